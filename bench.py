@@ -1,0 +1,440 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X decode hot path (one GPU).
+
+Workload (the configuration the headline metric is quoted on): Llama-3-8B
+decode, int4 group-64 linear layers. One step = one token through the 7
+projections of all 32 transformer layers (q, k, v, o 4096x4096 / 1024x4096,
+gate, up 14336x4096, down 4096x14336), every layer with its own weights, so
+the 3.93 GB of distinct weights defeat L2 and the 256 MB MALL. The step is
+captured once as a HIP graph (224 kernel launches) and replayed.
+
+`value` = algorithmic bytes per step / time (GB/s), algorithmic bytes =
+W + (scale, bias) + x + y(fp16) per GEMV. Also reported, each from its own
+timed region: per-shape GB/s, the roofline of the dominant kernel (the
+4096x14336 GEMV), the streaming-read ceiling, the gpt-oss-120b MoE block
+(36 layers x 128 experts resident, batch 1 and 8), VQ GEMV, the skinny-GEMM
+VALU/MFMA sweep, and the CPU baseline (the reference's CPU int4 path restated
+for x86, timed on this host).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sections ...]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+LLAMA = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+         ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+N_LAYERS = 32
+G = 64
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def int4_bytes(M, K, batch=1, G=G):
+    return M * K // 2 + M * (K // G) * 4 + 2 * batch * K + 2 * batch * M
+
+
+class Timer:
+    """HIP events on torch's current stream (where every libkq launch goes)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, fn, iters, warmup):
+        t = self.torch
+        for i in range(warmup):
+            fn(i)
+        t.cuda.synchronize()
+        e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(iters):
+            fn(warmup + i)
+        e1.record()
+        t.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters  # ms
+
+
+def graph_of(torch, fn):
+    """Capture fn() (a sequence of libkq launches) as a HIP graph."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm (first-launch code object loading) outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+# ---------------------------------------------------------------------------
+def make_int4_layers(torch, dev, n_layers, shapes, seed=1234):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    layers = []
+    for _ in range(n_layers):
+        L = {}
+        for name, M, K in shapes:
+            W = torch.randint(-2**31, 2**31 - 1, (M, K // 8), dtype=torch.int32, device=dev,
+                              generator=gen)
+            S = (torch.randn((M, K // G), device=dev, generator=gen) * 0.02).abs()
+            B = torch.randn((M, K // G), device=dev, generator=gen) * 0.02
+            SB = torch.stack([S, B], -1).half().contiguous()
+            L[name] = (W, SB, M, K)
+        layers.append(L)
+    return layers
+
+
+def bench_int4_step(torch, kq, dev, args, timer, res):
+    layers = make_int4_layers(torch, dev, N_LAYERS, LLAMA)
+    x = {K: (torch.randn((1, K), device=dev)).half() for K in (4096, 14336)}
+    y = {M: torch.empty((1, M), dtype=torch.float16, device=dev) for M in (1024, 4096, 14336)}
+    step_bytes = sum(int4_bytes(M, K) for _, M, K in LLAMA) * N_LAYERS
+
+    def step():
+        for L in layers:
+            for name, _, _ in LLAMA:
+                W, SB, M, K = L[name]
+                kq.int4_gemv(W, SB, x[K], y[M], kq.GemvParams(M, K, G))
+
+    # eager (Python launch loop) for reference
+    eager_ms = timer.run(lambda i: step(), 3, 1)
+    g = graph_of(torch, step)
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    res["step"] = dict(ms=ms, bytes=step_bytes, gbs=step_bytes / ms / 1e6, eager_ms=eager_ms)
+
+    # per-shape: one graph per shape over the 32 layer copies
+    per = {}
+    for name, M, K in LLAMA:
+        if name in ("k", "o", "up"):
+            continue  # same shape as v, q, gate
+
+        def one(name=name, M=M, K=K):
+            for L in layers:
+                W, SB, _, _ = L[name]
+                kq.int4_gemv(W, SB, x[K], y[M], kq.GemvParams(M, K, G))
+        gs = graph_of(torch, one)
+        reps = max(3, args.steps // 2)
+        us = timer.run(lambda i: gs.replay(), reps, 2) * 1e3 / N_LAYERS
+        b = int4_bytes(M, K)
+        per[f"{M}x{K}"] = dict(us=round(us, 3), gbs=round(b / us / 1e3, 1),
+                               frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4), bytes=b)
+    res["per_shape"] = per
+    del layers, g
+    torch.cuda.empty_cache()
+
+
+def bench_ceiling(torch, kq, dev, timer, res):
+    """Streaming read of the down-projection byte count, rotated over 32
+    distinct buffers (same protocol as the GEMV)."""
+    n = int4_bytes(4096, 14336) // 16 * 16
+    bufs = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(N_LAYERS)]
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+
+    def one():
+        for b in bufs:
+            kq.stream_read(b, n, sink)
+    g = graph_of(torch, one)
+    us = timer.run(lambda i: g.replay(), 10, 2) * 1e3 / N_LAYERS
+    res["ceiling"] = dict(bytes=n, us=round(us, 3), gbs=round(n / us / 1e3, 1))
+    big = 1 << 30
+    bb = torch.empty(big, dtype=torch.uint8, device=dev)
+    us = timer.run(lambda i: kq.stream_read(bb, big, sink), 10, 2) * 1e3
+    res["ceiling_1GiB"] = dict(bytes=big, us=round(us, 1), gbs=round(big / us / 1e3, 1))
+    del bufs, bb
+
+
+def bench_roofline(torch, kq, dev, timer, res):
+    """The dominant kernel: int4 GEMV at 4096 x 14336 (33 MB per launch),
+    launched back to back over 32 weight copies on torch's current stream."""
+    M, K = 4096, 14336
+    layers = make_int4_layers(torch, dev, N_LAYERS, [("down", M, K)], seed=99)
+    x = torch.randn((1, K), device=dev).half()
+    y = torch.empty((1, M), dtype=torch.float16, device=dev)
+
+    def one():
+        for L in layers:
+            W, SB, _, _ = L["down"]
+            kq.int4_gemv(W, SB, x, y, kq.GemvParams(M, K, G))
+    g = graph_of(torch, one)
+    reps = 20
+    us = timer.run(lambda i: g.replay(), reps, 3) * 1e3 / N_LAYERS
+    b = int4_bytes(M, K)
+    res["roofline"] = {"bound": "hbm", "achieved": round(b / us / 1e3, 1), "peak": HBM_PEAK_GBS,
+                       "unit": "GB/s", "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                       "traffic": None, "kernel": "int4_gemv_valu (4096x14336, batch 1)",
+                       "bytes_per_launch": b, "us_per_launch": round(us, 3),
+                       "launches_timed": reps * N_LAYERS}
+    del layers
+
+
+# ---------------------------------------------------------------------------
+def make_moe_pools(torch, dev, n_layers, d, seed=7):
+    """n_layers x n_experts expert blobs (gpt-oss layout) generated on the
+    GPU: uniform nibbles, bf16 scale ~ |N(0.0064, 0.001)|, bias ~ N(-0.048,
+    0.004), output bias ~ N(0, 0.02) (the statistics of int4-quantised
+    N(0, 0.02) weights)."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    ne = d.n_experts
+    pools = []
+    for _ in range(n_layers):
+        p = torch.randint(0, 256, (ne, d.blob), dtype=torch.uint8, device=dev, generator=gen)
+        for off, rows, cols in ((d.off_gate, d.inter, d.hidden), (d.off_up, d.inter, d.hidden),
+                                (d.off_down, d.hidden, d.inter)):
+            ng = rows * (cols // 64)
+            s = (torch.randn((ne, ng), device=dev, generator=gen) * 0.001 + 0.0064).abs()
+            b = torch.randn((ne, ng), device=dev, generator=gen) * 0.004 - 0.048
+            bi = torch.randn((ne, rows), device=dev, generator=gen) * 0.02
+            for sub, t in ((d.sub_s, s), (d.sub_b, b), (d.sub_bi, bi)):
+                raw = t.bfloat16().contiguous().view(torch.uint8)
+                p[:, off + sub: off + sub + raw.shape[1]] = raw
+        pools.append(p)
+    return pools
+
+
+def bench_moe(torch, kq, dev, args, timer, res, n_layers=36):
+    d = kq.moe_default_desc()
+    pools = make_moe_pools(torch, dev, n_layers, d)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    Rs = [(torch.randn((d.n_experts, d.hidden), device=dev, generator=gen) * 0.02).half()
+          for _ in range(n_layers)]
+    out = {}
+    for batch in (1, 8):
+        xs = [torch.randn((batch, d.hidden), device=dev, generator=gen).half()
+              for _ in range(n_layers)]
+        idx = torch.zeros((n_layers, batch, d.top_k), dtype=torch.int32, device=dev)
+        wgt = torch.zeros((n_layers, batch, d.top_k), dtype=torch.float32, device=dev)
+        H = torch.zeros((batch, d.top_k, d.inter), dtype=torch.float16, device=dev)
+        Y = torch.zeros((batch, d.hidden), dtype=torch.float32, device=dev)
+        nws = kq.moe_workspace_size(d, batch)
+        ws = torch.empty(nws, dtype=torch.uint8, device=dev)
+        kq.moe_workspace_init(ws, nws)
+
+        def step():
+            for l in range(n_layers):
+                kq.moe_block(pools[l], d, Rs[l], xs[l], idx[l], wgt[l], H, Y, ws, nws,
+                             batch=batch)
+        g = graph_of(torch, step)
+        ms = timer.run(lambda i: g.replay(), max(5, args.steps // 4), 2)
+        # bytes actually read: the distinct selected experts' 3 projections
+        # + router, per layer
+        ids = idx.cpu().numpy()
+        uniq = sum(len(set(ids[l].ravel().tolist())) for l in range(n_layers))
+        per_exp = 3 * (d.hidden * d.inter // 2 + 2 * 2 * d.inter * (d.hidden // 64) + 2 * d.inter)
+        router = d.n_experts * d.hidden * 2
+        b = uniq * per_exp + n_layers * router
+        us_block = ms * 1e3 / n_layers
+        out[f"batch{batch}"] = dict(us_per_block=round(us_block, 3),
+                                    us_per_token_per_block=round(us_block / batch, 3),
+                                    unique_experts_per_block=round(uniq / n_layers, 2),
+                                    bytes_per_block=int(b / n_layers),
+                                    gbs=round(b / (ms * 1e-3) / 1e9, 1),
+                                    frac=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+        del g
+    res["moe"] = out
+    del pools
+    torch.cuda.empty_cache()
+
+
+def bench_vq(torch, kq, dev, args, timer, res):
+    out = {}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    for M, K in ((14336, 4096), (4096, 14336)):
+        mats = []
+        for _ in range(N_LAYERS):
+            IDX = torch.randint(0, 256, (M, K // 2), dtype=torch.uint8, device=dev, generator=gen)
+            C = (torch.randn((M // 256, 256, 2), device=dev, generator=gen) * 0.02).half()
+            S = (torch.randn((M, 1), device=dev, generator=gen) * 0.1 + 1).abs().half()
+            mats.append((IDX, C, S))
+        x = torch.randn((1, K), device=dev).half()
+        y = torch.empty((1, M), dtype=torch.float16, device=dev)
+
+        def one():
+            for IDX, C, S in mats:
+                kq.vq_gemv(IDX, C, S, x, y, kq.VQParams(M, K, 256, K))
+        g = graph_of(torch, one)
+        us = timer.run(lambda i: g.replay(), 10, 2) * 1e3 / N_LAYERS
+        b = M * K // 2 + 2 * M + (M // 256) * 1024 + 2 * K + 2 * M
+        out[f"{M}x{K}"] = dict(us=round(us, 3), gbs=round(b / us / 1e3, 1),
+                               frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4), bytes=b)
+        del mats, g
+    res["vq"] = out
+
+
+def bench_skinny(torch, kq, dev, args, timer, res):
+    out = {}
+    ncopy = 8
+    for M, K in ((28672, 8192), (8192, 28672)):
+        layers = make_int4_layers(torch, dev, ncopy, [("w", M, K)], seed=M)
+        for batch in (1, 2, 4, 8, 16):
+            x = torch.randn((batch, K), device=dev).half()
+            y = torch.empty((batch, M), dtype=torch.float16, device=dev)
+            row = {}
+            for pname, path in (("valu", kq.PATH_VALU), ("mfma", kq.PATH_MFMA)):
+                def one(path=path):
+                    for L in layers:
+                        W, SB, _, _ = L["w"]
+                        kq.int4_gemv(W, SB, x, y, kq.GemvParams(M, K, G), batch=batch, path=path)
+                try:
+                    one()
+                except kq.KQError:
+                    row[pname] = None
+                    continue
+                g = graph_of(torch, one)
+                us = timer.run(lambda i: g.replay(), 5, 1) * 1e3 / ncopy
+                b = int4_bytes(M, K, batch)
+                row[pname] = dict(us=round(us, 2), gbs=round(b / us / 1e3, 1))
+                del g
+            out[f"{M}x{K}_b{batch}"] = row
+        del layers
+        torch.cuda.empty_cache()
+    res["skinny"] = out
+
+
+def cpu_baseline(seconds):
+    """The reference's CPU int4 GEMV (cpu_gemv_neon, restated for x86 in
+    oracle/cpu_fast.c) over the same Llama layer shapes, on this host's
+    cores, for a bounded sample of about `seconds` of CPU work."""
+    import numpy as np
+
+    import oracle
+    from kernels_amd import gen
+    if not oracle.cpu_fast_supported():
+        return None
+    cores = len(os.sched_getaffinity(0))
+    cores = max(1, min(cores, 16))
+    ncopy = 3  # 369 MB of distinct weights per pass, beyond the host LLC
+    mats = []
+    for c in range(ncopy):
+        L = []
+        for name, M, K in LLAMA:
+            p = gen.int4_problem(M, K, G, seed=c * 10 + len(L))
+            L.append((p["W"], p["SB"], p["X"][0], M, K))
+        mats.append(L)
+    step_bytes = sum(int4_bytes(M, K) for _, M, K in LLAMA)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        for W, SB, X, M, K in mats[n % ncopy]:
+            oracle.int4_gemv_cpu_fast(W, SB, X, M, K, G, nthreads=cores)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    layer_s = el / n
+    return {"value": round(step_bytes / layer_s / 1e9, 2), "unit": "GB/s", "cores": cores,
+            "kind": "port",
+            "sample": f"{n} Llama-3-8B layers (7 int4 GEMVs each, {step_bytes / 1e6:.1f} MB) "
+                      f"over {ncopy} weight copies in {el:.1f} s; x86 AVX2+F16C restatement of "
+                      f"cpu_gemv_neon (hetero-gemv/src/cpu_gemv.h:88-103)",
+            "ms_per_layer": round(layer_s * 1e3, 3),
+            "ms_per_step_32_layers": round(layer_s * 1e3 * N_LAYERS, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--sections", default="step,ceiling,roofline,moe,vq,skinny,cpu")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(see DESIGN.md, 'How the path would shard'); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    sections = set(args.sections.split(","))
+
+    import torch
+    from kernels_amd import kq
+    kq.lib()
+    dev = torch.device("cuda:0")
+    timer = Timer(torch)
+    res = {}
+    t_start = time.time()
+    if "step" in sections:
+        log("[bench] int4 decode step (Llama-3-8B, 32 layers)")
+        bench_int4_step(torch, kq, dev, args, timer, res)
+        log(f"[bench] step {res['step']}")
+    if "ceiling" in sections:
+        log("[bench] stream-read ceiling")
+        bench_ceiling(torch, kq, dev, timer, res)
+        log(f"[bench] ceiling {res['ceiling']} {res['ceiling_1GiB']}")
+    if "roofline" in sections:
+        log("[bench] roofline kernel 4096x14336")
+        bench_roofline(torch, kq, dev, timer, res)
+        log(f"[bench] roofline {res['roofline']}")
+    if "moe" in sections:
+        log("[bench] MoE block, 36 layers x 128 experts")
+        bench_moe(torch, kq, dev, args, timer, res)
+        log(f"[bench] moe {res['moe']}")
+    if "vq" in sections:
+        log("[bench] VQ GEMV")
+        bench_vq(torch, kq, dev, args, timer, res)
+        log(f"[bench] vq {res['vq']}")
+    if "skinny" in sections:
+        log("[bench] skinny GEMM sweep")
+        bench_skinny(torch, kq, dev, args, timer, res)
+        log(f"[bench] skinny {res['skinny']}")
+    cpu = None
+    if "cpu" in sections:
+        log("[bench] CPU baseline")
+        cpu = cpu_baseline(args.cpu_seconds)
+        log(f"[bench] cpu {cpu}")
+
+    st = res.get("step", {})
+    line = {
+        "metric": "int4 GEMV achieved HBM GB/s & % of 8 TB/s; fused MoE block us/token",
+        "value": round(st.get("gbs", 0.0), 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(st.get("ms", 0.0), 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4 x f16 -> f32 acc, f16 out",
+        "data": "synthetic (seeded, generated on the GPU)",
+        "config": {"workload": "Llama-3-8B decode int4 g64 linear layers: 32 layers x 7 GEMVs "
+                               "(4096x4096 x2, 1024x4096 x2, 14336x4096 x2, 4096x14336), batch 1, "
+                               "HIP graph of one token step",
+                   "bytes_per_step": st.get("bytes"), "frac_of_8TBs": round(st.get("gbs", 0) /
+                                                                            HBM_PEAK_GBS, 4)},
+        "roofline": res.get("roofline"),
+        "cpu_baseline": cpu,
+        "per_shape": res.get("per_shape"),
+        "ceiling": res.get("ceiling"),
+        "ceiling_1GiB": res.get("ceiling_1GiB"),
+        "moe": res.get("moe"),
+        "vq": res.get("vq"),
+        "skinny": res.get("skinny"),
+        "eager_ms_per_step": round(st.get("eager_ms", 0.0), 3) if st else None,
+        "wall_s": round(time.time() - t_start, 1),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,202 @@
+/*
+ * kq.h -- C ABI of libkq, the MI355X (gfx950) decode hot path:
+ *   int4 group-affine GEMV / batched skinny GEMM, codebook (VQ) dequant-GEMV,
+ *   and the three-kernel MoE block (router top-k, gathered gate/up + SwiGLU,
+ *   gathered down + weighted combine).
+ *
+ * Every entry point is stream-ordered and asynchronous: it validates its
+ * arguments on the host, enqueues kernels on `stream` and returns. Nothing
+ * here allocates device memory, synchronises, prints or exits. All pointers
+ * are caller-owned device pointers (W, IDX and X 16-byte aligned). Errors are
+ * reported as kq_status; kq_last_hip_error() gives the HIP code behind
+ * KQ_EHIP.
+ *
+ * The reference (Apple Metal) exposes this path only as per-kernel call
+ * surfaces encoded by its Objective-C++ harnesses; each declaration below
+ * cites the kernel and the encode site it replaces (paths are relative to the
+ * reference repository root).
+ */
+#ifndef KQ_H
+#define KQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same type as hipStream_t; NULL is the default stream. */
+typedef struct ihipStream_t* kq_stream_t;
+
+typedef enum kq_status {
+    KQ_OK = 0,
+    KQ_EINVAL = 1,        /* shape or argument violates the format contract */
+    KQ_ENULL = 2,         /* a required pointer is NULL */
+    KQ_EALIGN = 3,        /* a pointer is not aligned as required */
+    KQ_EUNSUPPORTED = 4,  /* well-formed but not implemented (dtype, batch) */
+    KQ_EWORKSPACE = 5,    /* workspace NULL or smaller than required */
+    KQ_EHIP = 6           /* the HIP runtime rejected a launch */
+} kq_status;
+
+typedef enum kq_dtype { KQ_F16 = 0, KQ_BF16 = 1, KQ_F32 = 2 } kq_dtype;
+
+/* Kernel family used by kq_int4_gemv_path (0 picks by batch size). */
+typedef enum kq_int4_path { KQ_PATH_AUTO = 0, KQ_PATH_VALU = 1, KQ_PATH_MFMA = 2 } kq_int4_path;
+
+const char* kq_status_str(kq_status s);
+/* hipError_t of the last KQ_EHIP returned on this host thread (0 if none). */
+int kq_last_hip_error(void);
+/* Library version string, e.g. "kq 0.1 gfx950". */
+const char* kq_version(void);
+
+/* ------------------------------------------------------------------------
+ * int4 group-affine GEMV / skinny GEMM
+ *
+ *   Y[b, m] = sum_k (S[m, k/G] * q[m, k] + B[m, k/G]) * X[b, k]
+ *   q[m, k] = (W[m, k/8] >> 4*(k%8)) & 0xF          (low nibble = lowest k)
+ *
+ * W  : uint32 [M][K/8], row-major.
+ * S,B: per (row, group) scale and bias, dtype sb_dtype (KQ_F16 or KQ_BF16).
+ *      B == NULL selects the interleaved layout: S points at SB[M][K/G][2]
+ *      (scale, bias) pairs. B != NULL selects separate S[M][K/G], B[M][K/G].
+ * X  : fp16 [batch][K].  Y: [batch][M] of y_dtype (KQ_F16 or KQ_F32).
+ * Accumulation is fp32. Constraints: K % 512 == 0 (K % 32 == 0 when
+ * K % 512 != 0 is accepted for K <= 16384 as well), G in {32, 64, 128},
+ * K % G == 0, 1 <= batch <= 16, M >= 1.
+ *
+ * Replaces: gemv_int4_wide_unroll (v6, interleaved SB)
+ *   int4-gemv/src/kernels.metal:397-448, encoded by addGemv
+ *   int4-gemv/src/main.mm:353-377,404-408; and the split-S/B layout of
+ *   gemv_int4_scalar / gemv_int4_simd int4-gemv/src/kernels.metal:71-136.
+ *   batch > 1 has no reference kernel (it is the per-row batch-1 op).
+ * ------------------------------------------------------------------------ */
+kq_status kq_int4_gemv(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,
+                       const uint16_t* X, void* Y, kq_dtype y_dtype,
+                       uint32_t M, uint32_t K, uint32_t G, uint32_t batch,
+                       kq_stream_t stream);
+
+/* kq_int4_gemv with the kernel family forced (VALU dot2 path or MFMA
+ * 32x32x16 path); used to measure the crossover. Same contract. */
+kq_status kq_int4_gemv_path(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,
+                            const uint16_t* X, void* Y, kq_dtype y_dtype,
+                            uint32_t M, uint32_t K, uint32_t G, uint32_t batch,
+                            kq_int4_path path, kq_stream_t stream);
+
+/* Tuning entry point: kq_int4_gemv with the kernel family and launch shape
+ * forced. rows = rows per wave (VALU: 1 or 2) or 32-row tiles per wave
+ * (MFMA: 1 or 2); unroll = 64-chunk steps in flight (VALU: 1, 2, 4, 8) or
+ * quant groups in flight (MFMA: 1, 2, 4). Returns KQ_EUNSUPPORTED for a shape
+ * the family cannot run. Used by the benchmark sweeps. */
+kq_status kq_int4_gemv_cfg(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,
+                           const uint16_t* X, void* Y, kq_dtype y_dtype,
+                           uint32_t M, uint32_t K, uint32_t G, uint32_t batch,
+                           kq_int4_path path, int rows, int unroll, kq_stream_t stream);
+
+/* xs[b, j] = sum_{i<32} X[b, 32j + i] in fp32, for j < K/32.
+ * Replaces: xsum32 int4-gemv/src/kernels.metal:54-65 (encoded at
+ * int4-gemv/src/main.mm:247-258). kq_int4_gemv computes this itself. */
+kq_status kq_xsum32(const uint16_t* X, float* xs, uint32_t K, uint32_t batch,
+                    kq_stream_t stream);
+
+/* Streaming read of `bytes` (multiple of 16) from src, XOR-folded; writes to
+ * sink[0] only if the fold is all ones. The bandwidth ceiling.
+ * Replaces: stream_read int4-gemv/src/kernels.metal:260-283. */
+kq_status kq_stream_read(const void* src, size_t bytes, uint32_t* sink, kq_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Codebook (VQ, d = 2, 256 entries) dequant-GEMV
+ *
+ *   Y[b, m] = sum_i S[m, 2i / scale_group] *
+ *             ( C[m / rows_per_cb][IDX[m, i]][0] * X[b, 2i]
+ *             + C[m / rows_per_cb][IDX[m, i]][1] * X[b, 2i+1] )
+ *
+ * IDX: uint8 [M][K/2].  C: fp16 [ceil(M/rows_per_cb)][256][2].
+ * S  : fp16 [M][K/scale_group].  X: fp16 [batch][K].  Y: [batch][M].
+ * rows_per_cb = M and scale_group = 32 is the reference format;
+ * rows_per_cb = 256 and scale_group = K is the per-row-scale format.
+ * Constraints: K % 512 == 0, scale_group % 32 == 0, K % scale_group == 0,
+ * rows_per_cb >= 1, 1 <= batch <= 4.
+ *
+ * Replaces: gemv_vq_wide (v5) vq-gemv/src/kernels.metal:337-380, encoded by
+ *   addVQ vq-gemv/src/main.mm:266-286,308-312.
+ * ------------------------------------------------------------------------ */
+kq_status kq_vq_gemv(const uint8_t* IDX, const uint16_t* C, const uint16_t* S,
+                     const uint16_t* X, void* Y, kq_dtype y_dtype,
+                     uint32_t M, uint32_t K, uint32_t rows_per_cb, uint32_t scale_group,
+                     uint32_t batch, kq_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * MoE decode block (gpt-oss expert-blob format)
+ *
+ * pool: n_experts blobs of `blob` bytes. Within a blob, projection p (gate,
+ * up, down) starts at off_p; within a projection, W (uint32 [rows][cols/8]),
+ * S and B (bf16 [rows][cols/64]) and BI (bf16 [rows], output bias) start at
+ * sub_w / sub_s / sub_b / sub_bi. gate and up are [inter][hidden], down is
+ * [hidden][inter]. Group size is 64.
+ * Mirrors MoEParams moe-fused/src/kernels.metal:22-35 and the blob constants
+ * moe-fused/src/main.mm:23-25 (derived fields are computed, not passed).
+ * ------------------------------------------------------------------------ */
+typedef struct kq_moe_desc {
+    uint32_t hidden, inter, n_experts, top_k;
+    uint64_t blob;
+    uint64_t off_gate, off_up, off_down;
+    uint64_t sub_w, sub_s, sub_b, sub_bi;
+} kq_moe_desc;
+
+/* Fills the gpt-oss-120b values: hidden = inter = 2880, 128 experts, top-4,
+ * blob 14,024,704 B, offsets as in moe-fused/src/main.mm:23-25. */
+void kq_moe_default_desc(kq_moe_desc* d);
+
+/* Bytes of workspace the MoE entry points need for `batch` tokens. The
+ * workspace must be zero-filled once (kq_moe_workspace_init) before its first
+ * use; every call leaves it ready for the next. Calls sharing one workspace
+ * must be stream-ordered. */
+size_t kq_moe_workspace_size(const kq_moe_desc* d, uint32_t batch);
+kq_status kq_moe_workspace_init(void* ws, size_t bytes, kq_stream_t stream);
+
+/* Router logits (fp32 accumulation) for every token, top_k by repeated
+ * argmax (strictly greater wins, so the lowest index wins ties), softmax over
+ * the selected logits. idx: uint32 [batch][top_k] in descending-logit order;
+ * wgt: fp32 [batch][top_k]. If X is fp32, xh (fp16 [batch][hidden]) receives
+ * half(X) for the projections; xh may be NULL when X is fp16.
+ * R: [n_experts][hidden] of r_dtype (KQ_F16 or KQ_F32).
+ * Replaces: router_topk moe-fused/src/kernels.metal:121-163 (encoded at
+ *   moe-fused/src/main.mm:178-185); batch > 1 is new. */
+kq_status kq_moe_router_topk(const void* R, kq_dtype r_dtype, const void* X, kq_dtype x_dtype,
+                             uint32_t batch, const kq_moe_desc* d,
+                             uint32_t* idx, float* wgt, uint16_t* xh,
+                             void* ws, size_t ws_bytes, kq_stream_t stream);
+
+/* H[b][k][m] = fp16( swiglu(gate_e(xh_b)[m] + BIg[m], up_e(xh_b)[m] + BIu[m]) )
+ * for e = idx[b][k], with swiglu(g, u) = min(g,7)*sigmoid(1.702*min(g,7)) *
+ * (clamp(u,-7,7) + 1). Each selected expert's rows are read once for all the
+ * tokens that chose it. H: fp16 [batch][top_k][inter].
+ * Replaces: fused_gate_up_swiglu moe-fused/src/kernels.metal:177-215
+ *   (encoded at moe-fused/src/main.mm:187-194). */
+kq_status kq_moe_gate_up_swiglu(const uint8_t* pool, const kq_moe_desc* d,
+                                const uint32_t* idx, const uint16_t* xh, uint16_t* H,
+                                uint32_t batch, void* ws, size_t ws_bytes, kq_stream_t stream);
+
+/* Y[b][m] = sum_k wgt[b][k] * (down_e(H[b][k])[m] + BId[m]), e = idx[b][k],
+ * summed in k order. Y: [batch][hidden] of y_dtype (KQ_F32 or KQ_F16).
+ * Replaces: fused_down_combine moe-fused/src/kernels.metal:224-265
+ *   (encoded at moe-fused/src/main.mm:196-204). */
+kq_status kq_moe_down_combine(const uint8_t* pool, const kq_moe_desc* d,
+                              const uint32_t* idx, const float* wgt, const uint16_t* H,
+                              void* Y, kq_dtype y_dtype, uint32_t batch,
+                              void* ws, size_t ws_bytes, kq_stream_t stream);
+
+/* The three passes back to back on one stream (encodeFused,
+ * moe-fused/src/main.mm:176-206). idx, wgt, xh (if X is fp32) and H are
+ * caller-provided outputs/intermediates of the sizes above. */
+kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d,
+                       const void* R, kq_dtype r_dtype, const void* X, kq_dtype x_dtype,
+                       uint32_t batch, uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H,
+                       void* Y, kq_dtype y_dtype, void* ws, size_t ws_bytes,
+                       kq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KQ_H */

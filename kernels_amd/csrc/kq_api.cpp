@@ -1,0 +1,266 @@
+// kq_api.cpp -- the extern "C" boundary of libkq (declared in include/kq.h).
+//
+// Validation happens here, on the host, before anything is enqueued: a
+// malformed shape becomes KQ_EINVAL, never an out-of-bounds kernel. Launch
+// failures become KQ_EHIP with the HIP code kept per host thread. Nothing
+// here allocates, synchronises, prints or exits (the reference harness's die()
+// -> exit(1), int4-gemv/src/main.mm:38-42, is the caller's business now).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+
+#include "kq.h"
+#include "kq_internal.h"
+
+namespace {
+
+thread_local int g_last_hip = 0;
+
+kq_status hip_status(hipError_t e) {
+    if (e == hipSuccess) return KQ_OK;
+    g_last_hip = (int)e;
+    return KQ_EHIP;
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+bool pow2(uint32_t v) { return v && !(v & (v - 1)); }
+
+kq_status check_int4(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,
+                     const uint16_t* X, void* Y, kq_dtype y_dtype, uint32_t M, uint32_t K,
+                     uint32_t G, uint32_t batch) {
+    if (!W || !S || !X || !Y) return KQ_ENULL;
+    if (M == 0 || K == 0 || batch == 0 || batch > 16) return KQ_EINVAL;
+    if (K % 32 != 0) return KQ_EINVAL;
+    if (!(G == 32 || G == 64 || G == 128) || K % G != 0) return KQ_EINVAL;
+    if ((uint64_t)M * (K / 8) > 0xFFFFFFFFull * 4) return KQ_EINVAL;
+    if (!(sb_dtype == KQ_F16 || sb_dtype == KQ_BF16)) return KQ_EUNSUPPORTED;
+    if (!(y_dtype == KQ_F16 || y_dtype == KQ_F32)) return KQ_EUNSUPPORTED;
+    if (!aligned(W, 16) || !aligned(X, 16)) return KQ_EALIGN;
+    if (B == nullptr ? !aligned(S, 4) : (!aligned(S, 2) || !aligned(B, 2))) return KQ_EALIGN;
+    if (!aligned(Y, y_dtype == KQ_F32 ? 4 : 2)) return KQ_EALIGN;
+    return KQ_OK;
+}
+
+kq_status run_int4(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,
+                   const uint16_t* X, void* Y, kq_dtype y_dtype, uint32_t M, uint32_t K,
+                   uint32_t G, uint32_t batch, kq_int4_path path, const kq::Int4Cfg* forced,
+                   kq_stream_t stream) {
+    kq_status st = check_int4(W, S, B, sb_dtype, X, Y, y_dtype, M, K, G, batch);
+    if (st != KQ_OK) return st;
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int mk = sb_dtype == KQ_BF16 ? 1 : 0;
+    const bool inter = B == nullptr;
+    const auto* Sp = static_cast<const uint16_t*>(S);
+    const auto* Bp = static_cast<const uint16_t*>(B);
+    const bool yf = y_dtype == KQ_F32;
+
+    kq::Int4Cfg vcfg = forced ? *forced : kq::int4_valu_default(M, K, batch);
+    kq::Int4Cfg mcfg = forced ? *forced : kq::int4_mfma_default(M, K, batch);
+    const bool valu_ok = kq::int4_valu_supported(K, batch, vcfg);
+    const bool mfma_ok = kq::int4_mfma_supported(K, G, batch, mcfg);
+    if (path == KQ_PATH_AUTO) path = (batch >= 8 && mfma_ok) || !valu_ok ? KQ_PATH_MFMA : KQ_PATH_VALU;
+    if (path == KQ_PATH_VALU) {
+        if (!valu_ok) return KQ_EUNSUPPORTED;
+        return hip_status(kq::launch_int4_valu(W, Sp, Bp, mk, inter, X, Y, yf, M, K, G, batch, vcfg, s));
+    }
+    if (path == KQ_PATH_MFMA) {
+        if (!mfma_ok) return KQ_EUNSUPPORTED;
+        return hip_status(kq::launch_int4_mfma(W, Sp, Bp, mk, inter, X, Y, yf, M, K, G, batch, mcfg, s));
+    }
+    return KQ_EINVAL;
+}
+
+kq_status check_desc(const kq_moe_desc* d, uint32_t batch) {
+    if (!d) return KQ_ENULL;
+    if (batch == 0 || batch > 16) return KQ_EINVAL;
+    if (d->n_experts == 0 || d->n_experts > 256) return KQ_EINVAL;
+    if (d->top_k == 0 || d->top_k > 8 || d->top_k > d->n_experts) return KQ_EINVAL;
+    if (d->hidden == 0 || d->inter == 0 || d->hidden % 64 || d->inter % 64) return KQ_EINVAL;
+    if (d->hidden > 4096 || d->inter > 4096) return KQ_EUNSUPPORTED;
+    // every sub-tensor of every projection must fit in the blob
+    const uint64_t rows_gu = d->inter, cols_gu = d->hidden, rows_dn = d->hidden, cols_dn = d->inter;
+    auto proj_ok = [&](uint64_t off, uint64_t rows, uint64_t cols) {
+        const uint64_t wb = rows * cols / 2, sb = rows * (cols / 64) * 2, bib = rows * 2;
+        return off + d->sub_w + wb <= d->blob && off + d->sub_s + sb <= d->blob &&
+               off + d->sub_b + sb <= d->blob && off + d->sub_bi + bib <= d->blob &&
+               (off + d->sub_w) % 16 == 0 && (off + d->sub_s) % 2 == 0 &&
+               (off + d->sub_b) % 2 == 0 && (off + d->sub_bi) % 2 == 0;
+    };
+    if (!proj_ok(d->off_gate, rows_gu, cols_gu) || !proj_ok(d->off_up, rows_gu, cols_gu) ||
+        !proj_ok(d->off_down, rows_dn, cols_dn))
+        return KQ_EINVAL;
+    if (d->blob % 16 != 0) return KQ_EALIGN;
+    return KQ_OK;
+}
+
+kq_status check_ws(const kq_moe_desc* d, uint32_t batch, const void* ws, size_t ws_bytes) {
+    if (!ws) return KQ_EWORKSPACE;
+    if (ws_bytes < kq::moe_ws_bytes(*d, batch)) return KQ_EWORKSPACE;
+    if (!aligned(ws, 256)) return KQ_EALIGN;
+    return KQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* kq_status_str(kq_status s) {
+    switch (s) {
+        case KQ_OK: return "ok";
+        case KQ_EINVAL: return "invalid argument (shape or format contract)";
+        case KQ_ENULL: return "null pointer";
+        case KQ_EALIGN: return "misaligned pointer";
+        case KQ_EUNSUPPORTED: return "unsupported configuration";
+        case KQ_EWORKSPACE: return "workspace missing or too small";
+        case KQ_EHIP: return "HIP launch error";
+    }
+    return "unknown status";
+}
+
+int kq_last_hip_error(void) { return g_last_hip; }
+
+const char* kq_version(void) { return "kq 0.1 gfx950"; }
+
+kq_status kq_int4_gemv(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,
+                       const uint16_t* X, void* Y, kq_dtype y_dtype, uint32_t M, uint32_t K,
+                       uint32_t G, uint32_t batch, kq_stream_t stream) {
+    return run_int4(W, S, B, sb_dtype, X, Y, y_dtype, M, K, G, batch, KQ_PATH_AUTO, nullptr, stream);
+}
+
+kq_status kq_int4_gemv_path(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,
+                            const uint16_t* X, void* Y, kq_dtype y_dtype, uint32_t M, uint32_t K,
+                            uint32_t G, uint32_t batch, kq_int4_path path, kq_stream_t stream) {
+    if (!(path == KQ_PATH_AUTO || path == KQ_PATH_VALU || path == KQ_PATH_MFMA)) return KQ_EINVAL;
+    return run_int4(W, S, B, sb_dtype, X, Y, y_dtype, M, K, G, batch, path, nullptr, stream);
+}
+
+kq_status kq_int4_gemv_cfg(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,
+                           const uint16_t* X, void* Y, kq_dtype y_dtype, uint32_t M, uint32_t K,
+                           uint32_t G, uint32_t batch, kq_int4_path path, int rows, int unroll,
+                           kq_stream_t stream) {
+    if (!(path == KQ_PATH_VALU || path == KQ_PATH_MFMA)) return KQ_EINVAL;
+    const kq::Int4Cfg cfg{rows, unroll};
+    return run_int4(W, S, B, sb_dtype, X, Y, y_dtype, M, K, G, batch, path, &cfg, stream);
+}
+
+kq_status kq_xsum32(const uint16_t* X, float* xs, uint32_t K, uint32_t batch, kq_stream_t stream) {
+    if (!X || !xs) return KQ_ENULL;
+    if (K == 0 || K % 32 || batch == 0) return KQ_EINVAL;
+    if (!aligned(X, 16) || !aligned(xs, 4)) return KQ_EALIGN;
+    return hip_status(kq::launch_xsum32(X, xs, K, batch, reinterpret_cast<hipStream_t>(stream)));
+}
+
+kq_status kq_stream_read(const void* src, size_t bytes, uint32_t* sink, kq_stream_t stream) {
+    if (!src || !sink) return KQ_ENULL;
+    if (bytes == 0 || bytes % 16) return KQ_EINVAL;
+    if (!aligned(src, 16)) return KQ_EALIGN;
+    return hip_status(kq::launch_stream_read(src, bytes, sink, reinterpret_cast<hipStream_t>(stream)));
+}
+
+kq_status kq_vq_gemv(const uint8_t* IDX, const uint16_t* C, const uint16_t* S, const uint16_t* X,
+                     void* Y, kq_dtype y_dtype, uint32_t M, uint32_t K, uint32_t rows_per_cb,
+                     uint32_t scale_group, uint32_t batch, kq_stream_t stream) {
+    if (!IDX || !C || !S || !X || !Y) return KQ_ENULL;
+    if (M == 0 || K == 0 || K % 32 || batch == 0 || batch > 16 || rows_per_cb == 0)
+        return KQ_EINVAL;
+    if (K / 32 * 64 * 1ull > 60000) return KQ_EUNSUPPORTED;  // x must fit the LDS stage
+    if (scale_group != K && (!pow2(scale_group) || scale_group < 32 || K % scale_group))
+        return KQ_EINVAL;
+    if (!(y_dtype == KQ_F16 || y_dtype == KQ_F32)) return KQ_EUNSUPPORTED;
+    if (!aligned(IDX, 16) || !aligned(X, 16) || !aligned(C, 4) || !aligned(S, 2)) return KQ_EALIGN;
+    if (!aligned(Y, y_dtype == KQ_F32 ? 4 : 2)) return KQ_EALIGN;
+    return hip_status(kq::launch_vq(IDX, C, S, X, Y, y_dtype == KQ_F32, M, K, rows_per_cb,
+                                    scale_group, batch, reinterpret_cast<hipStream_t>(stream)));
+}
+
+void kq_moe_default_desc(kq_moe_desc* d) {
+    if (!d) return;
+    // gpt-oss-120b as repacked by moe-stream (moe-fused/src/main.mm:23-25,76)
+    d->hidden = 2880;
+    d->inter = 2880;
+    d->n_experts = 128;
+    d->top_k = 4;
+    d->blob = 14024704;
+    d->off_gate = 0;
+    d->off_up = 4671360;
+    d->off_down = 9342720;
+    d->sub_w = 0;
+    d->sub_s = 4147200;
+    d->sub_b = 4406400;
+    d->sub_bi = 4665600;
+}
+
+size_t kq_moe_workspace_size(const kq_moe_desc* d, uint32_t batch) {
+    if (check_desc(d, batch) != KQ_OK) return 0;
+    return kq::moe_ws_bytes(*d, batch);
+}
+
+kq_status kq_moe_workspace_init(void* ws, size_t bytes, kq_stream_t stream) {
+    if (!ws) return KQ_ENULL;
+    if (!aligned(ws, 256)) return KQ_EALIGN;
+    return hip_status(kq::launch_ws_zero(ws, bytes, reinterpret_cast<hipStream_t>(stream)));
+}
+
+kq_status kq_moe_router_topk(const void* R, kq_dtype r_dtype, const void* X, kq_dtype x_dtype,
+                             uint32_t batch, const kq_moe_desc* d, uint32_t* idx, float* wgt,
+                             uint16_t* xh, void* ws, size_t ws_bytes, kq_stream_t stream) {
+    kq_status st = check_desc(d, batch);
+    if (st != KQ_OK) return st;
+    if (!R || !X || !idx || !wgt) return KQ_ENULL;
+    if (!(r_dtype == KQ_F16 || r_dtype == KQ_F32) || !(x_dtype == KQ_F16 || x_dtype == KQ_F32))
+        return KQ_EUNSUPPORTED;
+    if (d->hidden % 8) return KQ_EINVAL;
+    if (!aligned(R, 16) || !aligned(X, 16) || !aligned(idx, 4) || !aligned(wgt, 4)) return KQ_EALIGN;
+    if (xh && !aligned(xh, 2)) return KQ_EALIGN;
+    if ((st = check_ws(d, batch, ws, ws_bytes)) != KQ_OK) return st;
+    return hip_status(kq::launch_moe_router(R, r_dtype == KQ_F32, X, x_dtype == KQ_F32, batch, *d,
+                                            idx, wgt, xh, ws,
+                                            reinterpret_cast<hipStream_t>(stream)));
+}
+
+kq_status kq_moe_gate_up_swiglu(const uint8_t* pool, const kq_moe_desc* d, const uint32_t* idx,
+                                const uint16_t* xh, uint16_t* H, uint32_t batch, void* ws,
+                                size_t ws_bytes, kq_stream_t stream) {
+    kq_status st = check_desc(d, batch);
+    if (st != KQ_OK) return st;
+    if (!pool || !idx || !xh || !H) return KQ_ENULL;
+    if (!aligned(pool, 16) || !aligned(xh, 16) || !aligned(H, 2) || !aligned(idx, 4))
+        return KQ_EALIGN;
+    (void)ws;
+    (void)ws_bytes;
+    return hip_status(kq::launch_moe_gate_up(pool, *d, idx, xh, H, batch,
+                                             reinterpret_cast<hipStream_t>(stream)));
+}
+
+kq_status kq_moe_down_combine(const uint8_t* pool, const kq_moe_desc* d, const uint32_t* idx,
+                              const float* wgt, const uint16_t* H, void* Y, kq_dtype y_dtype,
+                              uint32_t batch, void* ws, size_t ws_bytes, kq_stream_t stream) {
+    kq_status st = check_desc(d, batch);
+    if (st != KQ_OK) return st;
+    if (!pool || !idx || !wgt || !H || !Y) return KQ_ENULL;
+    if (!(y_dtype == KQ_F16 || y_dtype == KQ_F32)) return KQ_EUNSUPPORTED;
+    if (!aligned(pool, 16) || !aligned(H, 16) || !aligned(idx, 4) || !aligned(wgt, 4))
+        return KQ_EALIGN;
+    if (!aligned(Y, y_dtype == KQ_F32 ? 4 : 2)) return KQ_EALIGN;
+    if ((st = check_ws(d, batch, ws, ws_bytes)) != KQ_OK) return st;
+    return hip_status(kq::launch_moe_down(pool, *d, idx, wgt, H, Y, y_dtype == KQ_F32, batch, ws,
+                                          reinterpret_cast<hipStream_t>(stream)));
+}
+
+kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d, const void* R, kq_dtype r_dtype,
+                       const void* X, kq_dtype x_dtype, uint32_t batch, uint32_t* idx, float* wgt,
+                       uint16_t* xh, uint16_t* H, void* Y, kq_dtype y_dtype, void* ws,
+                       size_t ws_bytes, kq_stream_t stream) {
+    if (x_dtype == KQ_F32 && !xh) return KQ_ENULL;
+    kq_status st = kq_moe_router_topk(R, r_dtype, X, x_dtype, batch, d, idx, wgt, xh, ws, ws_bytes,
+                                      stream);
+    if (st != KQ_OK) return st;
+    const uint16_t* xin = x_dtype == KQ_F32 ? xh : static_cast<const uint16_t*>(X);
+    st = kq_moe_gate_up_swiglu(pool, d, idx, xin, H, batch, ws, ws_bytes, stream);
+    if (st != KQ_OK) return st;
+    return kq_moe_down_combine(pool, d, idx, wgt, H, Y, y_dtype, batch, ws, ws_bytes, stream);
+}
+
+}  // extern "C"

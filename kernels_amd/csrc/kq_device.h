@@ -1,0 +1,101 @@
+// kq_device.h -- device helpers shared by the gfx950 kernels of libkq.
+//
+// Nibble -> fp16 without a convert instruction: OR-ing a 4-bit value into the
+// mantissa of an fp16 constant gives an exact fp16 integer.
+//   0x6400 is 1024.0 (ulp 1):    nibble in bits 0-3  -> 1024 + n
+//   0x5400 is   64.0 (ulp 1/16): nibble in bits 4-7  ->   64 + n
+// For one packed word w (nibble j = weight j) the four half2 operands
+//   t0 = (w      & 0x000F000F) | 0x64006400  = (1024+n0, 1024+n4)
+//   t1 = (w      & 0x00F000F0) | 0x54005400  = (  64+n1,   64+n5)
+//   t2 = (w >> 8 & 0x000F000F) | 0x64006400  = (1024+n2, 1024+n6)
+//   t3 = (w >> 8 & 0x00F000F0) | 0x54005400  = (  64+n3,   64+n7)
+// cost one shift and four AND-OR ops per 8 weights. Dotted (fp32 accumulate)
+// with the matching activation pairs (x0,x4) (x1,x5) (x2,x6) (x3,x7) they give
+//   sum_j n_j x_j + 1024*(x0+x2+x4+x6) + 64*(x1+x3+x5+x7),
+// and the constant term ("xc", per word or per chunk) depends on x only, so it
+// is computed once per activation vector and subtracted per quant group.
+// All products are exact in fp32 (11-bit x 11-bit significands).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kq {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr uint32_t kLo = 0x000F000Fu, kHi = 0x00F000F0u;
+constexpr uint32_t kE1024 = 0x64006400u, kE64 = 0x54005400u;
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c,
+                                  false);
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ float bf2f(uint16_t h) {
+    return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// Metadata element decode: KIND 0 = fp16, 1 = bf16.
+template <int KIND>
+__device__ __forceinline__ float meta2f(uint16_t v) {
+    if constexpr (KIND == 1) return bf2f(v);
+    else return h2f(v);
+}
+
+// Sum over the 64 lanes of a wave (butterfly; every lane gets the total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+// Sum over aligned groups of `W` lanes (W a power of two <= 64).
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Permuted activation pairs of one 8-element word of x (fp16 bits, 4 dwords
+// (x0,x1) (x2,x3) (x4,x5) (x6,x7)) -> (x0,x4) (x1,x5) (x2,x6) (x3,x7).
+__device__ __forceinline__ u32x4 pair_perm(u32x4 v) {
+    u32x4 p;
+    p.x = (v.x & 0xFFFFu) | (v.z << 16);
+    p.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
+    p.z = (v.y & 0xFFFFu) | (v.w << 16);
+    p.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+    return p;
+}
+
+// Plain sum and offset constant of one 8-element word of x (see header).
+__device__ __forceinline__ void word_consts(u32x4 v, float& s, float& c) {
+    float f0 = h2f(v.x & 0xFFFF), f1 = h2f(v.x >> 16), f2 = h2f(v.y & 0xFFFF), f3 = h2f(v.y >> 16);
+    float f4 = h2f(v.z & 0xFFFF), f5 = h2f(v.z >> 16), f6 = h2f(v.w & 0xFFFF), f7 = h2f(v.w >> 16);
+    float ev = (f0 + f4) + (f2 + f6), od = (f1 + f5) + (f3 + f7);
+    s = ev + od;
+    c = 1024.0f * ev + 64.0f * od;
+}
+
+// Dot of one packed word (8 nibbles) with its permuted activation pairs.
+__device__ __forceinline__ float qdot8(uint32_t w, u32x4 p, float acc) {
+    uint32_t w8 = w >> 8;
+    acc = dot2((w & kLo) | kE1024, p.x, acc);
+    acc = dot2((w & kHi) | kE64, p.y, acc);
+    acc = dot2((w8 & kLo) | kE1024, p.z, acc);
+    acc = dot2((w8 & kHi) | kE64, p.w, acc);
+    return acc;
+}
+
+template <typename T>
+__device__ __forceinline__ T ldg_nt(const T* p) {
+    return __builtin_nontemporal_load(p);
+}
+
+}  // namespace kq

@@ -1,0 +1,51 @@
+// kq_internal.h -- host-side launchers shared between the kernel files and the
+// C ABI shim (kq_api.cpp). Launchers assume validated arguments.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "kq.h"
+
+namespace kq {
+
+struct Int4Cfg {
+    int rows;    // rows per wave (VALU) / row tiles of 32 per wave (MFMA)
+    int unroll;  // 64-chunk steps whose loads are issued before any is used
+};
+
+// Default launch shape for a problem (tuning table).
+Int4Cfg int4_valu_default(uint32_t M, uint32_t K, uint32_t batch);
+size_t int4_valu_lds_bytes(uint32_t K, uint32_t batch);
+
+hipError_t launch_int4_valu(const uint32_t* W, const uint16_t* S, const uint16_t* B, int meta_kind,
+                            bool interleaved, const uint16_t* X, void* Y, bool y_f32, uint32_t M,
+                            uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg, hipStream_t s);
+bool int4_valu_supported(uint32_t K, uint32_t batch, Int4Cfg cfg);
+
+hipError_t launch_int4_mfma(const uint32_t* W, const uint16_t* S, const uint16_t* B, int meta_kind,
+                            bool interleaved, const uint16_t* X, void* Y, bool y_f32, uint32_t M,
+                            uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg, hipStream_t s);
+bool int4_mfma_supported(uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg);
+Int4Cfg int4_mfma_default(uint32_t M, uint32_t K, uint32_t batch);
+
+hipError_t launch_xsum32(const uint16_t* X, float* xs, uint32_t K, uint32_t batch, hipStream_t s);
+hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t s);
+
+hipError_t launch_vq(const uint8_t* IDX, const uint16_t* C, const uint16_t* S, const uint16_t* X,
+                     void* Y, bool y_f32, uint32_t M, uint32_t K, uint32_t rows_per_cb,
+                     uint32_t scale_group, uint32_t batch, hipStream_t s);
+
+// MoE
+size_t moe_ws_bytes(const kq_moe_desc& d, uint32_t batch);
+hipError_t launch_ws_zero(void* ws, size_t bytes, hipStream_t s);
+hipError_t launch_moe_router(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
+                             const kq_moe_desc& d, uint32_t* idx, float* wgt, uint16_t* xh,
+                             void* ws, hipStream_t s);
+hipError_t launch_moe_gate_up(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
+                              const uint16_t* xh, uint16_t* H, uint32_t batch, hipStream_t s);
+hipError_t launch_moe_down(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
+                           const float* wgt, const uint16_t* H, void* Y, bool y_f32,
+                           uint32_t batch, void* ws, hipStream_t s);
+
+}  // namespace kq

@@ -1,0 +1,35 @@
+"""Build recipe for the CPU oracle (test infrastructure only).
+
+Compiles oracle/kqref.c (fp64 restatement of the reference CPU paths) and
+oracle/cpu_fast.c (x86 restatement of the reference's CPU int4 GEMV, the timed
+baseline) into oracle/_build/libkqref.so with gcc. No -ffast-math: the oracle
+relies on IEEE fp64 semantics.
+
+The reference's own CPU code cannot be compiled here (its CPU references sit in
+Objective-C++ translation units that import Metal/Foundation, and its fast
+CPU path needs arm_neon.h and Accelerate), so there is no oracle/_ref build.
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+OUT_DIR = os.path.join(HERE, "_build")
+LIB = os.path.join(OUT_DIR, "libkqref.so")
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(OUT_DIR, exist_ok=True)
+    srcs = [os.path.join(HERE, "kqref.c"), os.path.join(HERE, "cpu_fast.c")]
+    tmp = LIB + ".tmp"
+    cmd = ["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-pthread", "-Wall", "-Wextra",
+           "-Wno-unused-parameter", "-o", tmp] + srcs + ["-lm"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,130 @@
+"""libkq's C ABI on the CPU: it loads, exports every symbol include/kq.h
+declares, and rejects malformed calls on the host before any launch (these
+calls never reach the GPU, so they run without one)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from kernels_amd import kq
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FAKE = 0x10000  # 64 KiB-aligned non-null address; never dereferenced by these calls
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "kq.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_exactly_the_exports():
+    assert header_symbols() == sorted(kq.EXPORTS)
+
+
+def test_library_exports_every_symbol():
+    L = kq.lib()
+    for name in header_symbols():
+        assert hasattr(L, name), name
+
+
+def test_status_strings_and_version():
+    L = kq.lib()
+    assert L.kq_status_str(kq.KQ_OK) == b"ok"
+    assert b"null" in L.kq_status_str(kq.KQ_ENULL)
+    assert L.kq_version().startswith(b"kq ")
+    assert L.kq_last_hip_error() == 0
+
+
+def _int4(W=FAKE, S=FAKE, B=None, sbdt=kq.F16, X=FAKE, Y=FAKE, ydt=kq.F16, M=64, K=512, G=64,
+          batch=1):
+    return kq.lib().kq_int4_gemv(W, S, B, sbdt, X, Y, ydt, M, K, G, batch, None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(W=None), kq.KQ_ENULL), (dict(X=None), kq.KQ_ENULL), (dict(Y=None), kq.KQ_ENULL),
+    (dict(K=100), kq.KQ_EINVAL), (dict(K=0), kq.KQ_EINVAL), (dict(M=0), kq.KQ_EINVAL),
+    (dict(G=48), kq.KQ_EINVAL), (dict(G=256), kq.KQ_EINVAL), (dict(K=96, G=64), kq.KQ_EINVAL),
+    (dict(batch=0), kq.KQ_EINVAL), (dict(batch=17), kq.KQ_EINVAL),
+    (dict(sbdt=kq.F32), kq.KQ_EUNSUPPORTED), (dict(ydt=kq.BF16), kq.KQ_EUNSUPPORTED),
+    (dict(W=FAKE + 4), kq.KQ_EALIGN), (dict(X=FAKE + 8), kq.KQ_EALIGN),
+    (dict(S=FAKE + 2), kq.KQ_EALIGN), (dict(Y=FAKE + 2, ydt=kq.F32), kq.KQ_EALIGN),
+])
+def test_int4_rejects_on_host(kw, status):
+    assert _int4(**kw) == status
+
+
+def test_int4_path_and_cfg_reject_on_host():
+    L = kq.lib()
+    assert L.kq_int4_gemv_path(FAKE, FAKE, None, kq.F16, FAKE, FAKE, kq.F16, 64, 512, 64, 1, 7,
+                               None) == kq.KQ_EINVAL
+    assert L.kq_int4_gemv_cfg(FAKE, FAKE, None, kq.F16, FAKE, FAKE, kq.F16, 64, 512, 64, 1,
+                              kq.PATH_VALU, 3, 1, None) == kq.KQ_EUNSUPPORTED
+    assert L.kq_int4_gemv_cfg(FAKE, FAKE, None, kq.F16, FAKE, FAKE, kq.F16, 64, 512, 64, 1,
+                              kq.PATH_AUTO, 1, 1, None) == kq.KQ_EINVAL
+
+
+def test_vq_rejects_on_host():
+    L = kq.lib()
+    ok = dict(IDX=FAKE, C=FAKE, S=FAKE, X=FAKE, Y=FAKE, ydt=kq.F16, M=256, K=512, rpc=256,
+              sg=32, batch=1)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return L.kq_vq_gemv(a["IDX"], a["C"], a["S"], a["X"], a["Y"], a["ydt"], a["M"], a["K"],
+                            a["rpc"], a["sg"], a["batch"], None)
+    assert call(IDX=None) == kq.KQ_ENULL
+    assert call(K=100) == kq.KQ_EINVAL
+    assert call(sg=48) == kq.KQ_EINVAL
+    assert call(sg=16) == kq.KQ_EINVAL
+    assert call(rpc=0) == kq.KQ_EINVAL
+    assert call(batch=0) == kq.KQ_EINVAL
+    assert call(IDX=FAKE + 1) == kq.KQ_EALIGN
+
+
+def test_moe_desc_and_workspace():
+    d = kq.moe_default_desc()
+    assert (d.hidden, d.inter, d.n_experts, d.top_k, d.blob) == (2880, 2880, 128, 4, 14024704)
+    assert (d.off_up, d.off_down, d.sub_s, d.sub_b, d.sub_bi) == (4671360, 9342720, 4147200,
+                                                                  4406400, 4665600)
+    n1 = kq.moe_workspace_size(d, 1)
+    n8 = kq.moe_workspace_size(d, 8)
+    assert 0 < n1 < n8
+    bad = kq.moe_default_desc()
+    bad.top_k = 0
+    assert kq.lib().kq_moe_workspace_size(C.byref(bad), 1) == 0
+    bad = kq.moe_default_desc()
+    bad.sub_bi = bad.blob  # output bias would run past the blob
+    assert kq.lib().kq_moe_workspace_size(C.byref(bad), 1) == 0
+    assert kq.lib().kq_moe_workspace_size(C.byref(d), 17) == 0
+
+
+def test_moe_rejects_on_host():
+    L = kq.lib()
+    d = kq.moe_default_desc()
+    n = kq.moe_workspace_size(d, 1)
+    r = L.kq_moe_router_topk(FAKE, kq.F16, FAKE, kq.F16, 1, C.byref(d), FAKE, FAKE, None, FAKE,
+                             n - 1, None)
+    assert r == kq.KQ_EWORKSPACE
+    r = L.kq_moe_router_topk(FAKE, kq.F16, FAKE, kq.F16, 1, C.byref(d), FAKE, FAKE, None, None,
+                             n, None)
+    assert r == kq.KQ_EWORKSPACE
+    r = L.kq_moe_router_topk(FAKE, kq.BF16, FAKE, kq.F16, 1, C.byref(d), FAKE, FAKE, None, FAKE,
+                             n, None)
+    assert r == kq.KQ_EUNSUPPORTED
+    r = L.kq_moe_gate_up_swiglu(None, C.byref(d), FAKE, FAKE, FAKE, 1, FAKE, n, None)
+    assert r == kq.KQ_ENULL
+    r = L.kq_moe_down_combine(FAKE, C.byref(d), FAKE, FAKE, FAKE, FAKE, kq.BF16, 1, FAKE, n, None)
+    assert r == kq.KQ_EUNSUPPORTED
+    r = L.kq_moe_block(FAKE, C.byref(d), FAKE, kq.F16, FAKE, kq.F32, 1, FAKE, FAKE, None, FAKE,
+                       FAKE, kq.F32, FAKE, n, None)
+    assert r == kq.KQ_ENULL  # fp32 x needs an xh buffer
+    assert L.kq_moe_workspace_init(FAKE + 4, 64, None) == kq.KQ_EALIGN
+
+
+def test_stream_read_and_xsum_reject_on_host():
+    L = kq.lib()
+    assert L.kq_stream_read(FAKE, 100, FAKE, None) == kq.KQ_EINVAL
+    assert L.kq_stream_read(None, 1024, FAKE, None) == kq.KQ_ENULL
+    assert L.kq_xsum32(FAKE, FAKE, 100, 1, None) == kq.KQ_EINVAL

@@ -1,0 +1,127 @@
+"""int4 GEMV / skinny GEMM on the GPU through libkq's C ABI vs the fp64 oracle.
+
+Bar: fp16 (or fp32) outputs with fp32 accumulation within
+|got - ref| <= 1e-2 + 1e-3 |ref|; the reference harness's own metric
+max|d| / max|ref| < 2e-3 (int4-gemv/src/main.mm:475-479) is asserted too.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from kernels_amd import gen, kq
+from tests._util import assert_close, dev, inf_rel, to_f64
+
+pytestmark = pytest.mark.gpu
+
+
+def run_int4(p, device, layout="sb", sb_dtype=kq.F16, y_dtype=torch.float16, path=kq.PATH_AUTO,
+             rows=0, unroll=0, S=None, B=None):
+    M, K, G, batch = p["M"], p["K"], p["G"], p["batch"]
+    W = dev(p["W"], device)
+    X = dev(p["X"], device)
+    if layout == "sb":
+        Sd, Bd = dev(p["SB"] if S is None else S, device), None
+    else:
+        Sd, Bd = dev(p["S"] if S is None else S, device), dev(p["B"] if B is None else B, device)
+    Y = torch.full((batch, M), float("nan"), dtype=y_dtype, device=device)
+    kq.int4_gemv(W, Sd, X, Y, kq.GemvParams(M, K, G), B=Bd, batch=batch, sb_dtype=sb_dtype,
+                 path=path, rows=rows, unroll=unroll)
+    torch.cuda.synchronize()
+    return to_f64(Y)
+
+
+def ref_int4(p, layout="sb", sb_dtype=oracle.F16, S=None, B=None):
+    if layout == "sb":
+        return oracle.int4_gemv(p["W"], p["SB"] if S is None else S, None, p["X"], p["M"], p["K"],
+                                p["G"], 1, sb_dtype)
+    return oracle.int4_gemv(p["W"], p["S"] if S is None else S, p["B"] if B is None else B, p["X"],
+                            p["M"], p["K"], p["G"], 0, sb_dtype)
+
+
+def check(got, ref, what):
+    assert_close(got, ref, what=what)
+    assert inf_rel(got, ref) < 2e-3, what
+
+
+def test_config0_4096x4096(gpu):
+    p = gen.int4_problem(4096, 4096, 64, seed=12345)
+    ref = ref_int4(p)
+    got = run_int4(p, gpu)
+    check(got, ref, "4096x4096 fp16 y")
+    print(f"config0 inf-rel err {inf_rel(got, ref):.2e}")
+
+
+@pytest.mark.parametrize("M,K", [(1024, 4096), (14336, 4096), (4096, 14336)])
+def test_llama_layer_shapes(gpu, M, K):
+    p = gen.int4_problem(M, K, 64, seed=M + K)
+    check(run_int4(p, gpu), ref_int4(p), f"{M}x{K}")
+
+
+@pytest.mark.parametrize("layout", ["sb", "split"])
+@pytest.mark.parametrize("ydt", [torch.float16, torch.float32])
+def test_layouts_and_output_dtype(gpu, layout, ydt):
+    p = gen.int4_problem(1000, 2048, 64, seed=7, dist="ref")
+    check(run_int4(p, gpu, layout=layout, y_dtype=ydt), ref_int4(p, layout), f"{layout} {ydt}")
+
+
+def test_bf16_metadata(gpu):
+    p = gen.int4_problem(512, 1024, 64, seed=3)
+    rng = np.random.default_rng(0)
+    S = gen.bf16_bits(np.abs(rng.normal(0, 0.02, (512, 16))))
+    B = gen.bf16_bits(rng.normal(0, 0.02, (512, 16)))
+    SB = np.ascontiguousarray(np.stack([S, B], -1))
+    ref = oracle.int4_gemv(p["W"], S, B, p["X"], 512, 1024, 64, 0, oracle.BF16)
+    check(run_int4(p, gpu, layout="split", sb_dtype=kq.BF16, S=S, B=B), ref, "bf16 split")
+    check(run_int4(p, gpu, layout="sb", sb_dtype=kq.BF16, S=SB), ref, "bf16 sb")
+
+
+@pytest.mark.parametrize("G", [32, 64, 128])
+@pytest.mark.parametrize("M,K", [(1, 512), (7, 4096), (4097, 1024), (300, 2880), (65, 32 * 64),
+                                 (33, 28672)])
+def test_edge_shapes_and_groups(gpu, M, K, G):
+    if K % G:
+        pytest.skip("K % G")
+    p = gen.int4_problem(M, K, G, seed=M * 31 + K + G)
+    check(run_int4(p, gpu), ref_int4(p), f"M={M} K={K} G={G}")
+
+
+@pytest.mark.parametrize("batch", [2, 3, 4, 5, 8, 16])
+def test_batched_valu(gpu, batch):
+    p = gen.int4_problem(777, 4096, 64, batch=batch, seed=batch)
+    check(run_int4(p, gpu, path=kq.PATH_VALU), ref_int4(p), f"valu batch {batch}")
+
+
+@pytest.mark.parametrize("rows,unroll", [(1, 1), (1, 2), (1, 4), (1, 8), (2, 1), (2, 2), (2, 4),
+                                         (2, 8)])
+def test_forced_launch_shapes_agree(gpu, rows, unroll):
+    p = gen.int4_problem(1031, 8192, 64, seed=11)
+    ref = ref_int4(p)
+    got = run_int4(p, gpu, path=kq.PATH_VALU, rows=rows, unroll=unroll)
+    check(got, ref, f"rows={rows} unroll={unroll}")
+
+
+def test_deterministic(gpu):
+    p = gen.int4_problem(4096, 4096, 64, seed=5)
+    a = run_int4(p, gpu)
+    b = run_int4(p, gpu)
+    assert np.array_equal(a, b)
+
+
+def test_xsum32_bit_exact(gpu):
+    rng = np.random.default_rng(2)
+    K, batch = 14336, 3
+    X = gen.f16_bits(rng.normal(0, 1, (batch, K)))
+    xs = torch.empty((batch, K // 32), dtype=torch.float32, device=gpu)
+    kq.xsum32(dev(X, gpu), xs, K, batch)
+    torch.cuda.synchronize()
+    assert np.array_equal(xs.cpu().numpy(), oracle.xsum32(X, K))
+
+
+def test_stream_read_runs(gpu):
+    n = 64 << 20
+    src = torch.zeros(n // 4, dtype=torch.int32, device=gpu)
+    sink = torch.zeros(4, dtype=torch.int32, device=gpu)
+    kq.stream_read(src, n, sink)
+    torch.cuda.synchronize()
+    assert sink.cpu().tolist() == [0, 0, 0, 0]  # fold of zeros is not all ones

@@ -1,0 +1,197 @@
+"""MoE block (router top-k, gathered gate/up + SwiGLU, gathered down +
+combine) on the GPU through libkq's C ABI vs the fp64 oracle.
+
+Routing is held bit-exact (indices equal, and order); softmax weights within
+1e-6; h and y within |d| <= 1e-2 + 1e-3 |ref|, plus the reference's own
+max|d| / max|y| < 2e-3 (moe-fused/src/main.mm:356-375)."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from kernels_amd import gen, kq
+from tests._util import assert_close, dev, host_bits, inf_rel, to_f64
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def odesc(d):
+    o = oracle.MoEDesc()
+    for f, _ in kq.MoEDesc._fields_:
+        setattr(o, f, getattr(d, f))
+    return o
+
+
+class Block:
+    """Device buffers for one block call."""
+
+    def __init__(self, device, d, batch, x_f32=False, y_dtype=torch.float32):
+        self.d, self.batch = d, batch
+        self.idx = torch.zeros((batch, d.top_k), dtype=torch.int32, device=device)
+        self.wgt = torch.zeros((batch, d.top_k), dtype=torch.float32, device=device)
+        self.H = torch.zeros((batch, d.top_k, d.inter), dtype=torch.float16, device=device)
+        self.y = torch.full((batch, d.hidden), float("nan"), dtype=y_dtype, device=device)
+        self.xh = torch.zeros((batch, d.hidden), dtype=torch.float16, device=device) if x_f32 else None
+        self.wsb = kq.moe_workspace_size(d, batch)
+        self.ws = torch.empty(self.wsb, dtype=torch.uint8, device=device)
+        kq.moe_workspace_init(self.ws, self.wsb)
+
+
+@pytest.fixture(scope="module")
+def pool16(gpu):
+    """16 experts of real gpt-oss shape, weights quantised from N(0, 0.02)."""
+    host = gen.moe_pool(16, seed=31, quantize=True)
+    return host, dev(host, gpu)
+
+
+def routing_margin(lg, k):
+    s = np.sort(lg, axis=-1)[..., ::-1]
+    return float(np.min(s[..., k - 1] - s[..., k]))
+
+
+def test_router_golden_lcg(gpu):
+    """moe-fused/results/topk.txt reproduced on the GPU (fp32 R and x)."""
+    spec = json.load(open(os.path.join(GOLD, "moe_topk_lcg.json")))
+    d = kq.moe_default_desc()
+    R, X = gen.moe_lcg_inputs()
+    b = Block(gpu, d, 1, x_f32=True)
+    Rd = torch.from_numpy(R).to(gpu)
+    Xd = torch.from_numpy(X).to(gpu)
+    kq.moe_router_topk(Rd, Xd, b.idx, b.wgt, d, b.ws, b.wsb, batch=1, xh=b.xh)
+    torch.cuda.synchronize()
+    assert b.idx.cpu().tolist()[0] == spec["expected_idx"]
+    assert np.allclose(b.wgt.cpu().numpy()[0], spec["expected_wgt"], atol=1e-6, rtol=0)
+    assert np.array_equal(host_bits(b.xh, np.uint16), X.astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("batch", [1, 3, 8, 16])
+def test_router_fp16_exact(gpu, batch):
+    d = kq.moe_default_desc()
+    R, X = gen.moe_inputs(128, batch=batch, seed=100 + batch)
+    idx, wgt, lg = oracle.moe_router(R, oracle.F16, X, oracle.F16, batch, odesc(d))
+    assert routing_margin(lg, 4) > 1e-4, "test data too close to a tie"
+    b = Block(gpu, d, batch)
+    kq.moe_router_topk(dev(R, gpu).view(torch.float16), dev(X, gpu).view(torch.float16), b.idx,
+                       b.wgt, d, b.ws, b.wsb, batch=batch)
+    torch.cuda.synchronize()
+    assert np.array_equal(b.idx.cpu().numpy().astype(np.uint32), idx)
+    assert np.allclose(b.wgt.cpu().numpy(), wgt, atol=1e-6, rtol=0)
+
+
+def test_router_ties_lowest_index(gpu):
+    """Exactly tied logits: the lowest expert index wins (strict > scan)."""
+    d = kq.moe_default_desc()
+    d.n_experts, d.top_k = 16, 4
+    R = np.zeros((16, 2880), np.float32)
+    R[[3, 9, 12], 0] = 2.0          # three-way tie for first
+    R[[5, 6], 0] = 1.0              # tie for fourth: 5 wins
+    X = np.zeros((1, 2880), np.float32)
+    X[0, 0] = 1.0
+    b = Block(gpu, d, 1, x_f32=True)
+    kq.moe_router_topk(torch.from_numpy(R).to(gpu), torch.from_numpy(X).to(gpu), b.idx, b.wgt, d,
+                       b.ws, b.wsb, batch=1, xh=b.xh)
+    torch.cuda.synchronize()
+    oidx, owgt, _ = oracle.moe_router(R, oracle.F32, X, oracle.F32, 1, odesc(d))
+    assert b.idx.cpu().tolist()[0] == [3, 9, 12, 5] == oidx[0].tolist()
+    assert np.allclose(b.wgt.cpu().numpy()[0], owgt[0], atol=1e-6)
+
+
+def _pool_desc(n):
+    d = kq.moe_default_desc()
+    d.n_experts = n
+    return d
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_gate_up_and_down_vs_oracle(gpu, pool16, batch):
+    host, pool = pool16
+    d = _pool_desc(16)
+    rng = np.random.default_rng(batch)
+    idx = np.stack([rng.choice(16, 4, replace=False) for _ in range(batch)]).astype(np.uint32)
+    wgt = rng.dirichlet(np.ones(4), batch)
+    X = gen.f16_bits(rng.normal(0, 1, (batch, 2880)))
+    b = Block(gpu, d, batch)
+    idx_d = dev(idx, gpu)
+    wgt_d = torch.from_numpy(wgt.astype(np.float32)).to(gpu)
+    kq.moe_gate_up_swiglu(pool, d, idx_d, dev(X, gpu), b.H, b.ws, b.wsb, batch=batch)
+    torch.cuda.synchronize()
+    Href = oracle.moe_gate_up(host, odesc(d), idx, X, oracle.F16, batch)
+    Hgot = to_f64(b.H)
+    assert_close(Hgot, Href, what="h")
+    # down from the GPU's own fp16 h, weights as fp32 exactly as the GPU sees them
+    kq.moe_down_combine(pool, d, idx_d, wgt_d, b.H, b.y, b.ws, b.wsb, batch=batch)
+    torch.cuda.synchronize()
+    Yref = oracle.moe_down(host, odesc(d), idx, wgt.astype(np.float32).astype(np.float64),
+                           host_bits(b.H, np.uint16), batch)
+    assert_close(to_f64(b.y), Yref, atol=1e-4, rtol=1e-4, what="down+combine")
+
+
+def test_duplicate_and_shared_experts(gpu, pool16):
+    """Slots that select the same expert (within and across tokens) read its
+    rows once and still land in their own h / y slots."""
+    host, pool = pool16
+    d = _pool_desc(16)
+    idx = np.array([[3, 3, 7, 1], [7, 3, 2, 15], [1, 1, 1, 1]], np.uint32)
+    wgt = np.array([[0.4, 0.3, 0.2, 0.1], [0.25] * 4, [0.1, 0.2, 0.3, 0.4]])
+    batch = 3
+    X = gen.f16_bits(np.random.default_rng(4).normal(0, 1, (batch, 2880)))
+    b = Block(gpu, d, batch)
+    kq.moe_gate_up_swiglu(pool, d, dev(idx, gpu), dev(X, gpu), b.H, b.ws, b.wsb, batch=batch)
+    kq.moe_down_combine(pool, d, dev(idx, gpu), torch.from_numpy(wgt.astype(np.float32)).to(gpu),
+                        b.H, b.y, b.ws, b.wsb, batch=batch)
+    torch.cuda.synchronize()
+    Href = oracle.moe_gate_up(host, odesc(d), idx, X, oracle.F16, batch)
+    assert_close(to_f64(b.H), Href, what="h dup")
+    Yref = oracle.moe_down(host, odesc(d), idx, wgt.astype(np.float32).astype(np.float64),
+                           host_bits(b.H, np.uint16), batch)
+    assert_close(to_f64(b.y), Yref, atol=1e-4, rtol=1e-4, what="y dup")
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_block_full_pool(gpu, batch):
+    """Config 4: 128 experts of gpt-oss-120b shape (1.8 GB resident), top-4,
+    fp16 router and x; the block vs the fp64 block reference."""
+    host = gen.moe_pool(128, seed=55, quantize=False)
+    pool = dev(host, gpu)
+    d = kq.moe_default_desc()
+    R, X = gen.moe_inputs(128, batch=batch, seed=9 + batch)
+    oidx, owgt, lg = oracle.moe_router(R, oracle.F16, X, oracle.F16, batch, odesc(d))
+    assert routing_margin(lg, 4) > 1e-4
+    _, _, Yref = oracle.moe_block(host, odesc(d), R, oracle.F16, X, oracle.F16, batch)
+    b = Block(gpu, d, batch)
+    Rd, Xd = dev(R, gpu).view(torch.float16), dev(X, gpu).view(torch.float16)
+    for rep in range(3):  # workspace counters must reset between calls
+        b.y.fill_(float("nan"))
+        kq.moe_block(pool, d, Rd, Xd, b.idx, b.wgt, b.H, b.y, b.ws, b.wsb, batch=batch)
+        torch.cuda.synchronize()
+        assert np.array_equal(b.idx.cpu().numpy().astype(np.uint32), oidx)
+        assert np.allclose(b.wgt.cpu().numpy(), owgt, atol=1e-6)
+        got = to_f64(b.y)
+        assert_close(got, Yref, what=f"block batch {batch} rep {rep}")
+        assert inf_rel(got, Yref) < 2e-3
+    del pool
+
+
+def test_block_fp32_inputs_and_fp16_out(gpu, pool16):
+    """Reference-fidelity inputs: fp32 router and x (xh written by the router)."""
+    host, pool = pool16
+    d = _pool_desc(16)
+    rng = np.random.default_rng(12)
+    R = (rng.normal(0, 0.02, (16, 2880))).astype(np.float32)
+    X = rng.normal(0, 1, (2, 2880)).astype(np.float32)
+    oidx, owgt, lg = oracle.moe_router(R, oracle.F32, X, oracle.F32, 2, odesc(d))
+    assert routing_margin(lg, 4) > 1e-4
+    b = Block(gpu, d, 2, x_f32=True, y_dtype=torch.float16)
+    kq.moe_block(pool, d, torch.from_numpy(R).to(gpu), torch.from_numpy(X).to(gpu), b.idx, b.wgt,
+                 b.H, b.y, b.ws, b.wsb, batch=2, xh=b.xh)
+    torch.cuda.synchronize()
+    assert np.array_equal(b.idx.cpu().numpy().astype(np.uint32), oidx)
+    # the reference CPU block uses x unrounded; the GPU projections use half(x)
+    _, _, Yref = oracle.moe_block(host, odesc(d), R, oracle.F32, X, oracle.F32, 2)
+    got = to_f64(b.y)
+    assert inf_rel(got, Yref) < 2e-3
+    assert_close(got, Yref, atol=2e-2, rtol=2e-3, what="fp32-in block")

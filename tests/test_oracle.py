@@ -1,0 +1,309 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it.
+
+Every oracle function is checked against at least one of: the reference's
+golden vector (moe-fused/results/topk.txt), a closed form, a special case
+that reduces to a textbook routine (numpy fp64 matmul of an independently
+dequantised matrix), or brute force on tiny inputs. Inputs are chosen so that
+a plausible mistake (wrong nibble order, wrong group index, bias applied per
+chunk instead of per group, transposed codeword, tie broken the wrong way,
+SwiGLU clamp on the wrong side) fails one of them.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from kernels_amd import gen
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# ---------------------------------------------------------------- conversions
+def test_f16_decode_all_patterns():
+    L = oracle.lib()
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = bits.view(np.float16).astype(np.float64)
+    got = np.array([L.kqref_f16_to_f64(int(b)) for b in bits[::97]])
+    r = ref[::97]
+    same = (got == r) | (np.isnan(got) & np.isnan(r))
+    assert same.all()
+
+
+def test_f32_to_f16_rounding_matches_numpy():
+    L = oracle.lib()
+    rng = np.random.default_rng(1)
+    vals = np.concatenate([rng.normal(0, 1, 2000), rng.normal(0, 1e-5, 500), rng.normal(0, 3e4, 500),
+                           [0.0, -0.0, 65504.0, 65520.0, 1e9, -1e9, 5.96e-8, 2.98e-8, 1.0 + 2**-11,
+                            1.0 + 3 * 2**-11]]).astype(np.float32)
+    want = vals.astype(np.float16).view(np.uint16)
+    got = np.array([L.kqref_f32_to_f16(float(v)) for v in vals], dtype=np.uint16)
+    assert (got == want).all()
+
+
+def test_bf16_decode_and_round():
+    L = oracle.lib()
+    assert L.kqref_bf16_to_f64(0x3F80) == 1.0
+    assert L.kqref_bf16_to_f64(0xC040) == -3.0
+    assert L.kqref_bf16_to_f64(0x0001) == np.float32(np.uint32(1 << 16).view(np.float32))
+    # generator rounding: round to nearest even on the dropped 16 bits
+    # (bf16 ulp at 1.0 is 2^-7: 1 + 2^-8 is a tie -> even (down), 1 + 3*2^-8
+    # a tie -> even (up), 1 + 3*2^-9 above half -> up)
+    x = np.array([1.0, 1.0 + 2**-8, 1.0 + 3 * 2**-8, 1.0 + 3 * 2**-9], np.float32)
+    b = gen.bf16_bits(x)
+    assert b.tolist() == [0x3F80, 0x3F80, 0x3F82, 0x3F81]
+
+
+# --------------------------------------------------------------------- int4
+def _unpack_np(W, K):
+    """Independent nibble unpack: q[m, k] = (W[m, k//8] >> 4*(k%8)) & 15."""
+    k = np.arange(K)
+    return ((W[:, k // 8] >> (4 * (k % 8)).astype(np.uint32)) & 0xF).astype(np.float64)
+
+
+def _dequant_np(p):
+    M, K, G = p["M"], p["K"], p["G"]
+    q = _unpack_np(p["W"], K)
+    s = gen.f16_bits(0) * 0 + p["S"].view(np.float16).astype(np.float64)
+    b = p["B"].view(np.float16).astype(np.float64)
+    g = np.arange(K) // G
+    return s[:, g] * q + b[:, g]
+
+
+def test_int4_nibble_order_closed_form():
+    # word 0x76543210 -> q[k] = k % 8; with S=1, B=0, x = e_k, y = q[:, k]
+    M, K, G = 3, 64, 32
+    W = np.full((M, K // 8), 0x76543210, np.uint32)
+    W[1] = 0xFEDCBA98
+    W[2, 3] = 0x0000000F  # k = 24 -> 15, k = 25..31 -> 0
+    one, zero = gen.f16_bits(1.0), gen.f16_bits(0.0)
+    S = np.full((M, K // G), one, np.uint16)
+    B = np.full((M, K // G), zero, np.uint16)
+    for k in (0, 1, 5, 7, 8, 24, 25, 63):
+        X = np.zeros((1, K), np.uint16)
+        X[0, k] = one
+        y = oracle.int4_gemv(W, S, B, X, M, K, G, sb_interleaved=0)[0]
+        want = [k % 8, 8 + k % 8, (k % 8) if k // 8 != 3 else (15 if k == 24 else 0)]
+        assert y.tolist() == want, (k, y, want)
+
+
+def test_int4_bias_once_per_group_closed_form():
+    # all q = 0 -> y = sum_g B_g * sum_{k in g} x_k ; distinct B per group pins the group index
+    M, K, G = 2, 256, 64
+    W = np.zeros((M, K // 8), np.uint32)
+    S = np.full((M, K // G), gen.f16_bits(0.5), np.uint16)
+    Bv = np.array([[1, 2, 4, 8], [-1, 0.5, 0.25, 3]], np.float32)
+    B = gen.f16_bits(Bv)
+    X = gen.f16_bits(np.arange(K, dtype=np.float32)[None] / 64.0)
+    y = oracle.int4_gemv(W, S, B, X, M, K, G, sb_interleaved=0)[0]
+    xs = np.arange(K).reshape(K // G, G).sum(1) / 64.0
+    assert np.array_equal(y, (Bv.astype(np.float64) * xs).sum(1))
+
+
+def test_int4_x_ones_closed_form():
+    # x = 1 -> y = sum_k (S q + B)
+    p = gen.int4_problem(8, 128, 64, seed=3)
+    X = np.full((1, 128), gen.f16_bits(1.0), np.uint16)
+    y = oracle.int4_gemv(p["W"], p["S"], p["B"], X, 8, 128, 64, sb_interleaved=0)[0]
+    assert np.allclose(y, _dequant_np(p).sum(1), rtol=1e-13, atol=1e-13)
+
+
+@pytest.mark.parametrize("M,K,G,batch", [(7, 512, 32, 1), (5, 1024, 64, 2), (9, 512, 128, 3),
+                                         (16, 2880, 64, 1)])
+def test_int4_matches_numpy_dequant_matmul(M, K, G, batch):
+    p = gen.int4_problem(M, K, G, batch=batch, seed=M * K + G)
+    ref = p["X"].view(np.float16).astype(np.float64) @ _dequant_np(p).T
+    y_split = oracle.int4_gemv(p["W"], p["S"], p["B"], p["X"], M, K, G, sb_interleaved=0)
+    y_inter = oracle.int4_gemv(p["W"], p["SB"], None, p["X"], M, K, G, sb_interleaved=1)
+    assert np.allclose(y_split, ref, rtol=1e-12, atol=1e-12)
+    assert np.array_equal(y_split, y_inter)
+
+
+def test_int4_bf16_metadata():
+    M, K, G = 4, 256, 64
+    p = gen.int4_problem(M, K, G, seed=9)
+    s = np.abs(np.random.default_rng(2).normal(0, 0.02, (M, K // G))).astype(np.float32)
+    b = np.random.default_rng(3).normal(0, 0.02, (M, K // G)).astype(np.float32)
+    Sb, Bb = gen.bf16_bits(s), gen.bf16_bits(b)
+    sd = (Sb.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    bd = (Bb.astype(np.uint32) << 16).view(np.float64 if False else np.float32).astype(np.float64)
+    g = np.arange(K) // G
+    Wd = sd[:, g] * _unpack_np(p["W"], K) + bd[:, g]
+    ref = p["X"].view(np.float16).astype(np.float64) @ Wd.T
+    y = oracle.int4_gemv(p["W"], Sb, Bb, p["X"], M, K, G, sb_interleaved=0, sb_dtype=oracle.BF16)
+    assert np.allclose(y, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_xsum32_order():
+    rng = np.random.default_rng(5)
+    K = 4096
+    X = gen.f16_bits(rng.normal(0, 100, (2, K)))
+    got = oracle.xsum32(X, K)
+    x = X.view(np.float16).astype(np.float32).reshape(2, K // 32, 8, 4)
+    want = np.zeros((2, K // 32), np.float32)
+    for i in range(8):
+        t = (x[..., i, 0] + x[..., i, 1]) + x[..., i, 2]
+        t = t + x[..., i, 3]
+        want = want + t
+    assert np.array_equal(got, want)
+    # and it is the chunk sum to fp32 accuracy
+    assert np.allclose(got, x.reshape(2, K // 32, 32).astype(np.float64).sum(-1), rtol=1e-5,
+                       atol=1e-2)
+
+
+# ----------------------------------------------------------------------- VQ
+def _vq_dequant_np(p):
+    M, K, rpc, sg = p["M"], p["K"], p["rows_per_cb"], p["scale_group"]
+    C = p["C"].view(np.float16).astype(np.float64)
+    S = p["S"].view(np.float16).astype(np.float64)
+    Wd = np.zeros((M, K))
+    for m in range(M):
+        cw = C[m // rpc][p["IDX"][m]]  # [K/2][2]
+        Wd[m] = cw.reshape(K) * np.repeat(S[m], sg)
+    return Wd
+
+
+def test_vq_index_readback_closed_form():
+    # C[c] = (c, 0), S = 1, x = e_{2i} -> y = IDX[:, i]; x = e_{2i+1} -> 0
+    M, K = 4, 512
+    rng = np.random.default_rng(0)
+    IDX = rng.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    C = np.zeros((1, 256, 2), np.uint16)
+    C[0, :, 0] = gen.f16_bits(np.arange(256))
+    S = np.full((M, K // 32), gen.f16_bits(1.0), np.uint16)
+    for i in (0, 1, 17, 255):
+        X = np.zeros((1, K), np.uint16)
+        X[0, 2 * i] = gen.f16_bits(1.0)
+        y = oracle.vq_gemv(IDX, C, S, X, M, K, M, 32)[0]
+        assert y.tolist() == IDX[:, i].astype(float).tolist()
+        X[0, 2 * i], X[0, 2 * i + 1] = 0, gen.f16_bits(1.0)
+        y = oracle.vq_gemv(IDX, C, S, X, M, K, M, 32)[0]
+        assert y.tolist() == [0.0] * M
+
+
+@pytest.mark.parametrize("M,K,rpc,sg,batch", [(8, 512, 8, 32, 1), (20, 1024, 8, 1024, 2),
+                                              (9, 512, 4, 64, 1), (300, 512, 256, 512, 1)])
+def test_vq_matches_numpy(M, K, rpc, sg, batch):
+    p = gen.vq_problem(M, K, rows_per_cb=rpc, scale_group=sg, batch=batch, seed=M + K)
+    ref = p["X"].view(np.float16).astype(np.float64) @ _vq_dequant_np(p).T
+    y = oracle.vq_gemv(p["IDX"], p["C"], p["S"], p["X"], M, K, rpc, sg)
+    assert np.allclose(y, ref, rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------------- MoE
+def _desc(n_experts=128, top_k=4):
+    d = oracle.MoEDesc()
+    d.hidden, d.inter, d.n_experts, d.top_k = 2880, 2880, n_experts, top_k
+    d.blob = gen.MOE_BLOB
+    for k, v in gen.MOE_OFF.items():
+        setattr(d, k, v)
+    return d
+
+
+def test_router_golden_vector():
+    """moe-fused/results/topk.txt from the reference's LCG inputs."""
+    spec = json.load(open(os.path.join(GOLD, "moe_topk_lcg.json")))
+    lines = open(os.path.join(GOLD, "moe_topk_lcg.txt")).read().split("\n")
+    fix = [l.split() for l in lines if l.strip()]
+    R, X = gen.moe_lcg_inputs()
+    idx, wgt, lg = oracle.moe_router(R, oracle.F32, X, oracle.F32, 1, _desc())
+    assert idx[0].tolist() == [int(a) for a, _ in fix] == spec["expected_idx"]
+    assert np.allclose(wgt[0], [float(b) for _, b in fix], atol=1e-7, rtol=0)
+    srt = np.sort(lg[0])[::-1]
+    assert srt[3] - srt[4] > 1e-3  # fixture is tie-robust
+
+
+def test_router_ties_lowest_index_and_order():
+    d = _desc(n_experts=8, top_k=3)
+    d.hidden = 8
+    # logits = R @ x with x = e_0 -> logits = R[:, 0]
+    R = np.zeros((8, 8), np.float32)
+    R[:, 0] = [1.0, 3.0, 2.0, 3.0, -1.0, 2.0, 0.0, 3.0]
+    X = np.zeros((1, 8), np.float32)
+    X[0, 0] = 1.0
+    idx, wgt, _ = oracle.moe_router(R, oracle.F32, X, oracle.F32, 1, d)
+    assert idx[0].tolist() == [1, 3, 7]  # three-way tie at 3.0: ascending index
+    assert np.allclose(wgt[0], [1 / 3] * 3)
+    R[:, 0] = [1.0, 5.0, 2.0, 3.0, -1.0, 2.0, 0.0, 4.0]
+    idx, wgt, _ = oracle.moe_router(R, oracle.F32, X, oracle.F32, 1, d)
+    assert idx[0].tolist() == [1, 7, 3]
+    e = np.exp(np.array([5.0, 4.0, 3.0]) - 5.0)
+    assert np.allclose(wgt[0], e / e.sum(), rtol=1e-15)
+
+
+def test_swiglu_closed_forms():
+    sg = oracle.swiglu
+    assert sg(0.0, 3.0) == 0.0
+    # gate clamps at 7 from above only; up clamps to [-7, 7]
+    top = 7.0 / (1.0 + np.exp(-1.702 * 7.0))
+    assert sg(100.0, 0.0) == pytest.approx(top)
+    assert sg(7.0, 100.0) == pytest.approx(top * 8.0)
+    assert sg(7.0, -100.0) == pytest.approx(top * -6.0)
+    g = -3.0
+    assert sg(g, 1.0) == pytest.approx(g / (1 + np.exp(1.702 * 3.0)) * 2.0)
+
+
+def test_moe_proj_matches_numpy():
+    rng = np.random.default_rng(11)
+    blob = gen.moe_expert_blob(rng, quantize=True)
+    d = _desc()
+    x = rng.normal(0, 1, 2880)
+    for name in ("off_gate", "off_up", "off_down"):
+        base = gen.MOE_OFF[name]
+        W = blob[base:base + 4147200].view(np.uint32).reshape(2880, 360)
+        S = blob[base + 4147200:base + 4147200 + 259200].view(np.uint16).reshape(2880, 45)
+        B = blob[base + 4406400:base + 4406400 + 259200].view(np.uint16).reshape(2880, 45)
+        BI = blob[base + 4665600:base + 4665600 + 5760].view(np.uint16)
+        bf = lambda a: (a.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        g = np.arange(2880) // 64
+        Wd = bf(S)[:, g] * _unpack_np(W, 2880) + bf(B)[:, g]
+        ref = Wd @ x + bf(BI)
+        got = oracle.moe_proj(blob, base, d, x, 2880, 2880)
+        assert np.allclose(got, ref, rtol=1e-11, atol=1e-11), name
+
+
+def test_quantizer_reconstructs_within_half_step():
+    rng = np.random.default_rng(4)
+    w = rng.normal(0, 0.02, (16, 128)).astype(np.float32)
+    W, S, B = gen.quantize_affine_int4(w)
+    s = (S.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    b = (B.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    g = np.arange(128) // 64
+    wd = s[:, g] * _unpack_np(W, 128) + b[:, g]
+    assert np.all(np.abs(wd - w) <= 0.5 * s[:, g] + 0.02 * 2**-7 * 4)
+
+
+def test_moe_block_composes(tmp_path):
+    """Block = router -> top-k -> gate/up -> SwiGLU -> down -> combine,
+    recomposed here from the single-projection oracle and numpy."""
+    ne = 8
+    pool = gen.moe_pool(ne, seed=21, quantize=False)
+    d = _desc(n_experts=ne)
+    R, X = gen.moe_inputs(ne, batch=2, seed=5)
+    idx, wgt, Y = oracle.moe_block(pool, d, R, oracle.F16, X, oracle.F16, 2)
+    for b in range(2):
+        x = X[b].view(np.float16).astype(np.float64)
+        lg = R.view(np.float16).astype(np.float64) @ x
+        order = np.argsort(-lg, kind="stable")[:4]
+        assert idx[b].tolist() == order.tolist()
+        e = np.exp(lg[order] - lg[order].max())
+        assert np.allclose(wgt[b], e / e.sum(), rtol=1e-14)
+        y = np.zeros(2880)
+        for j, ex in enumerate(order):
+            bb = pool[ex * gen.MOE_BLOB:(ex + 1) * gen.MOE_BLOB]
+            g = oracle.moe_proj(bb, gen.MOE_OFF["off_gate"], d, x, 2880, 2880)
+            u = oracle.moe_proj(bb, gen.MOE_OFF["off_up"], d, x, 2880, 2880)
+            h = np.array([oracle.swiglu(a, c) for a, c in zip(g, u)])
+            y += wgt[b, j] * oracle.moe_proj(bb, gen.MOE_OFF["off_down"], d, h, 2880, 2880)
+        assert np.allclose(Y[b], y, rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------ CPU fast path
+@pytest.mark.skipif(not oracle.cpu_fast_supported(), reason="needs AVX2/FMA/F16C")
+def test_cpu_fast_matches_oracle():
+    M, K, G = 64, 4096, 64
+    p = gen.int4_problem(M, K, G, seed=8)
+    ref = oracle.int4_gemv(p["W"], p["SB"], None, p["X"], M, K, G, sb_interleaved=1)[0]
+    got = oracle.int4_gemv_cpu_fast(p["W"], p["SB"], p["X"][0], M, K, G, nthreads=2)
+    assert np.allclose(got, ref, rtol=1e-4, atol=1e-3)
