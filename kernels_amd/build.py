@@ -21,7 +21,8 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-         "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
+         "-Wall", "-Wextra", "-Wshadow", "-Werror=shadow", "-Werror=unused-parameter",
+         "-Wno-unused-function", "-Wno-sign-compare",
          "-I", os.path.join(ROOT, "include"), "-I", CSRC]
 
 

@@ -35,7 +35,6 @@ namespace {
 constexpr int kMoeThreads = 256;
 constexpr int kTileRows = 16;    // rows per workgroup (4 waves x 4 rows)
 constexpr int kSlotRound = 4;    // token slots staged per LDS round
-constexpr uint32_t kMaxSlots = 128;
 
 struct WsLayout {
     size_t cnt_router, cnt_tiles, lg, ys, total;
@@ -167,7 +166,7 @@ __global__ __launch_bounds__(128) void moe_router_k(const void* __restrict__ R,
             pick[j] = bi;
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                if (lane + 64 * q == bi) v[q] = -INFINITY;
+                if ((uint32_t)lane + 64 * q == bi) v[q] = -INFINITY;
         }
         if (lane == 0) {
             float mx = chosen[0];
@@ -238,8 +237,8 @@ __device__ __forceinline__ void stage_acts(const uint16_t* base, const uint32_t*
     const uint32_t nw = K >> 3, nch = K >> 5;
     const uint32_t total = (uint32_t)ns * nw;
     const int tid = threadIdx.x;
-    for (uint32_t base = 0; base < total; base += kMoeThreads) {
-        const uint32_t w = base + tid;
+    for (uint32_t w0 = 0; w0 < total; w0 += kMoeThreads) {
+        const uint32_t w = w0 + tid;
         const bool ok = w < total;
         const uint32_t t = ok ? w / nw : 0, wi = ok ? w - t * nw : 0;
         u32x4 v = ok ? *reinterpret_cast<const u32x4*>(base + (size_t)offs[t] + (size_t)wi * 8)
