@@ -61,9 +61,10 @@ const char* kq_version(void);
  *      B == NULL selects the interleaved layout: S points at SB[M][K/G][2]
  *      (scale, bias) pairs. B != NULL selects separate S[M][K/G], B[M][K/G].
  * X  : fp16 [batch][K].  Y: [batch][M] of y_dtype (KQ_F16 or KQ_F32).
- * Accumulation is fp32. Constraints: K % 512 == 0 (K % 32 == 0 when
- * K % 512 != 0 is accepted for K <= 16384 as well), G in {32, 64, 128},
- * K % G == 0, 1 <= batch <= 16, M >= 1.
+ * Accumulation is fp32. Constraints: K % 32 == 0, G in {32, 64, 128},
+ * K % G == 0, 1 <= batch <= 16, M >= 1. The activations are staged in LDS,
+ * which bounds K (K <= 29120 on the VALU path); a shape no path takes
+ * returns KQ_EUNSUPPORTED.
  *
  * Replaces: gemv_int4_wide_unroll (v6, interleaved SB)
  *   int4-gemv/src/kernels.metal:397-448, encoded by addGemv
@@ -84,10 +85,11 @@ kq_status kq_int4_gemv_path(const uint32_t* W, const void* S, const void* B, kq_
                             kq_int4_path path, kq_stream_t stream);
 
 /* Tuning entry point: kq_int4_gemv with the kernel family and launch shape
- * forced. rows = rows per wave (VALU: 1 or 2) or 32-row tiles per wave
- * (MFMA: 1 or 2); unroll = 64-chunk steps in flight (VALU: 1, 2, 4, 8) or
- * quant groups in flight (MFMA: 1, 2, 4). Returns KQ_EUNSUPPORTED for a shape
- * the family cannot run. Used by the benchmark sweeps. */
+ * forced. VALU: rows = rows per wave work item (1, 2, 4, 8), unroll = 64-chunk
+ * steps per row held in registers (1, 2, 4, 8, 16; at least K/2048).
+ * MFMA: rows = 32-row tiles per wave (1, 2), unroll = quant groups in flight
+ * (1, 2, 4). Returns KQ_EUNSUPPORTED for a shape the family cannot run. Used
+ * by the benchmark sweeps. */
 kq_status kq_int4_gemv_cfg(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,
                            const uint16_t* X, void* Y, kq_dtype y_dtype,
                            uint32_t M, uint32_t K, uint32_t G, uint32_t batch,
@@ -115,8 +117,9 @@ kq_status kq_stream_read(const void* src, size_t bytes, uint32_t* sink, kq_strea
  * S  : fp16 [M][K/scale_group].  X: fp16 [batch][K].  Y: [batch][M].
  * rows_per_cb = M and scale_group = 32 is the reference format;
  * rows_per_cb = 256 and scale_group = K is the per-row-scale format.
- * Constraints: K % 512 == 0, scale_group % 32 == 0, K % scale_group == 0,
- * rows_per_cb >= 1, 1 <= batch <= 4.
+ * Constraints: K % 32 == 0, K <= 30000 (x is staged in LDS, else
+ * KQ_EUNSUPPORTED), scale_group == K or a power of two >= 32 dividing K,
+ * rows_per_cb >= 1, 1 <= batch <= 16.
  *
  * Replaces: gemv_vq_wide (v5) vq-gemv/src/kernels.metal:337-380, encoded by
  *   addVQ vq-gemv/src/main.mm:266-286,308-312.
@@ -148,10 +151,11 @@ typedef struct kq_moe_desc {
  * blob 14,024,704 B, offsets as in moe-fused/src/main.mm:23-25. */
 void kq_moe_default_desc(kq_moe_desc* d);
 
-/* Bytes of workspace the MoE entry points need for `batch` tokens. The
- * workspace must be zero-filled once (kq_moe_workspace_init) before its first
- * use; every call leaves it ready for the next. Calls sharing one workspace
- * must be stream-ordered. */
+/* Bytes of workspace the MoE entry points need for `batch` tokens (the
+ * router logits). Its contents need no initialisation; kq_moe_workspace_init
+ * zero-fills it (a kernel, not a memset, so it can sit in a captured graph).
+ * Calls sharing one workspace must be stream-ordered. gate_up and down keep
+ * their intermediates on chip and accept a NULL workspace. */
 size_t kq_moe_workspace_size(const kq_moe_desc* d, uint32_t batch);
 kq_status kq_moe_workspace_init(void* ws, size_t bytes, kq_stream_t stream);
 

@@ -228,7 +228,7 @@ kq_status kq_moe_gate_up_swiglu(const uint8_t* pool, const kq_moe_desc* d, const
     if (!pool || !idx || !xh || !H) return KQ_ENULL;
     if (!aligned(pool, 16) || !aligned(xh, 16) || !aligned(H, 2) || !aligned(idx, 4))
         return KQ_EALIGN;
-    (void)ws;
+    (void)ws;  // this pass keeps everything on chip
     (void)ws_bytes;
     return hip_status(kq::launch_moe_gate_up(pool, *d, idx, xh, H, batch,
                                              reinterpret_cast<hipStream_t>(stream)));
@@ -244,8 +244,9 @@ kq_status kq_moe_down_combine(const uint8_t* pool, const kq_moe_desc* d, const u
     if (!aligned(pool, 16) || !aligned(H, 16) || !aligned(idx, 4) || !aligned(wgt, 4))
         return KQ_EALIGN;
     if (!aligned(Y, y_dtype == KQ_F32 ? 4 : 2)) return KQ_EALIGN;
-    if ((st = check_ws(d, batch, ws, ws_bytes)) != KQ_OK) return st;
-    return hip_status(kq::launch_moe_down(pool, *d, idx, wgt, H, Y, y_dtype == KQ_F32, batch, ws,
+    (void)ws;  // the combine happens in LDS
+    (void)ws_bytes;
+    return hip_status(kq::launch_moe_down(pool, *d, idx, wgt, H, Y, y_dtype == KQ_F32, batch,
                                           reinterpret_cast<hipStream_t>(stream)));
 }
 
@@ -253,14 +254,23 @@ kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d, const void* R,
                        const void* X, kq_dtype x_dtype, uint32_t batch, uint32_t* idx, float* wgt,
                        uint16_t* xh, uint16_t* H, void* Y, kq_dtype y_dtype, void* ws,
                        size_t ws_bytes, kq_stream_t stream) {
+    kq_status st = check_desc(d, batch);
+    if (st != KQ_OK) return st;
+    if (!pool || !R || !X || !idx || !wgt || !H || !Y) return KQ_ENULL;
     if (x_dtype == KQ_F32 && !xh) return KQ_ENULL;
-    kq_status st = kq_moe_router_topk(R, r_dtype, X, x_dtype, batch, d, idx, wgt, xh, ws, ws_bytes,
-                                      stream);
-    if (st != KQ_OK) return st;
-    const uint16_t* xin = x_dtype == KQ_F32 ? xh : static_cast<const uint16_t*>(X);
-    st = kq_moe_gate_up_swiglu(pool, d, idx, xin, H, batch, ws, ws_bytes, stream);
-    if (st != KQ_OK) return st;
-    return kq_moe_down_combine(pool, d, idx, wgt, H, Y, y_dtype, batch, ws, ws_bytes, stream);
+    if (!(r_dtype == KQ_F16 || r_dtype == KQ_F32) || !(x_dtype == KQ_F16 || x_dtype == KQ_F32))
+        return KQ_EUNSUPPORTED;
+    if (!(y_dtype == KQ_F16 || y_dtype == KQ_F32)) return KQ_EUNSUPPORTED;
+    if (d->hidden % 8) return KQ_EINVAL;
+    if (!aligned(pool, 16) || !aligned(R, 16) || !aligned(X, 16) || !aligned(idx, 4) ||
+        !aligned(wgt, 4) || !aligned(H, 16))
+        return KQ_EALIGN;
+    if (xh && !aligned(xh, 16)) return KQ_EALIGN;
+    if (!aligned(Y, y_dtype == KQ_F32 ? 4 : 2)) return KQ_EALIGN;
+    if ((st = check_ws(d, batch, ws, ws_bytes)) != KQ_OK) return st;
+    return hip_status(kq::launch_moe_block(pool, *d, R, r_dtype == KQ_F32, X, x_dtype == KQ_F32,
+                                           batch, idx, wgt, xh, H, Y, y_dtype == KQ_F32, ws,
+                                           reinterpret_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -49,17 +49,42 @@ __device__ __forceinline__ float meta2f(uint16_t v) {
     else return h2f(v);
 }
 
-// Sum over the 64 lanes of a wave (butterfly; every lane gets the total).
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// ---- wave64 reductions on DPP (no LDS round trip) ----
+// dpp_ctrl encodings (gfx9): quad_perm [1,0,3,2] = 0xB1 (xor 1),
+// [2,3,0,1] = 0x4E (xor 2); row_ror:n = 0x120 + n; row_bcast:15 = 0x142,
+// row_bcast:31 = 0x143.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                 ROW_MASK, 0xF, false));
+}
+// Sum over each row of 16 lanes; every lane of the row gets its row's sum.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x124>(v);
+    v += dpp_f<0x128>(v);
     return v;
 }
-// Sum over aligned groups of `W` lanes (W a power of two <= 64).
-template <int W>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Sum over the 64 lanes of a wave, returned uniformly (from lane 63).
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    v += dpp_f<0x142, 0xA>(v);  // rows 1, 3 += lane 15 / 47
+    v += dpp_f<0x143, 0xC>(v);  // rows 2, 3 += lane 31
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+// Sums over the two 32-lane halves of a wave: .x = lanes 0-31, .y = lanes 32-63.
+__device__ __forceinline__ float2 half_sums(float v) {
+    v = row16_sum(v);
+    v += dpp_f<0x142, 0xA>(v);  // lane 31 = rows 0+1, lane 63 = rows 2+3
+    return make_float2(
+        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 31)),
+        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63)));
+}
+// Sum over aligned groups of 4 lanes (every lane gets its group's sum).
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
     return v;
 }
 
@@ -83,9 +108,42 @@ __device__ __forceinline__ void word_consts(u32x4 v, float& s, float& c) {
     c = 1024.0f * ev + 64.0f * od;
 }
 
+// (a & b) | c. gfx9 VOP3 takes no literal operands, so with literal masks the
+// compiler splits this into v_and + v_or; with b and c held in VGPRs whose
+// values it cannot see (DequantConsts) it selects one v_and_or_b32. This stays
+// plain C on purpose: the hazard recognizer does not model inline asm, and an
+// asm VALU write into a register that an in-flight MFMA still reads as its A/B
+// operand (WAR) gets no wait states.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t b, uint32_t c) {
+    return (a & b) | c;
+}
+
+// The four dequant constants held in VGPRs.
+struct DequantConsts {
+    uint32_t lo, hi, e1024, e64;
+    __device__ __forceinline__ DequantConsts() {
+        // opaque to the optimiser so the values stay in VGPRs
+        asm("v_mov_b32 %0, %1" : "=v"(lo) : "i"(kLo));
+        asm("v_mov_b32 %0, %1" : "=v"(hi) : "i"(kHi));
+        asm("v_mov_b32 %0, %1" : "=v"(e1024) : "i"(kE1024));
+        asm("v_mov_b32 %0, %1" : "=v"(e64) : "i"(kE64));
+    }
+};
+
 // Dot of one packed word (8 nibbles) with its permuted activation pairs.
+__device__ __forceinline__ float qdot8(uint32_t w, u32x4 p, float acc, const DequantConsts& k) {
+    const uint32_t w8 = w >> 8;
+    acc = dot2(and_or(w, k.lo, k.e1024), p.x, acc);
+    acc = dot2(and_or(w, k.hi, k.e64), p.y, acc);
+    acc = dot2(and_or(w8, k.lo, k.e1024), p.z, acc);
+    acc = dot2(and_or(w8, k.hi, k.e64), p.w, acc);
+    return acc;
+}
+
+// Dot of one packed word with pairs (plain C; used where the register cost
+// of the constants matters more than two instructions).
 __device__ __forceinline__ float qdot8(uint32_t w, u32x4 p, float acc) {
-    uint32_t w8 = w >> 8;
+    const uint32_t w8 = w >> 8;
     acc = dot2((w & kLo) | kE1024, p.x, acc);
     acc = dot2((w & kHi) | kE64, p.y, acc);
     acc = dot2((w8 & kLo) | kE1024, p.z, acc);

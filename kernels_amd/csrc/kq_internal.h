@@ -46,6 +46,11 @@ hipError_t launch_moe_gate_up(const uint8_t* pool, const kq_moe_desc& d, const u
                               const uint16_t* xh, uint16_t* H, uint32_t batch, hipStream_t s);
 hipError_t launch_moe_down(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
                            const float* wgt, const uint16_t* H, void* Y, bool y_f32,
-                           uint32_t batch, void* ws, hipStream_t s);
+                           uint32_t batch, hipStream_t s);
+// router logits -> gate/up with in-kernel top-k (publishes idx, wgt) -> down
+hipError_t launch_moe_block(const uint8_t* pool, const kq_moe_desc& d, const void* R, bool r_f32,
+                            const void* X, bool x_f32, uint32_t batch, uint32_t* idx, float* wgt,
+                            uint16_t* xh, uint16_t* H, void* Y, bool y_f32, void* ws,
+                            hipStream_t s);
 
 }  // namespace kq

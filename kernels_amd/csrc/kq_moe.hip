@@ -1,30 +1,35 @@
-// kq_moe.hip -- the MoE decode block in three launches (gfx950).
+// kq_moe.hip -- the MoE decode block (gfx950).
 //
 // Reference: moe-fused/src/kernels.metal:98-265 (router_topk,
 // fused_gate_up_swiglu, fused_down_combine) and the block reference
 // moe-fused/src/main.mm:302-334. The block has two grid-wide dependencies
-// (idx before the expert gather; all of h before down), so it is three
-// kernels here too, each designed for CDNA4:
+// (the selected experts before the gather; all of h before down). On CDNA4
+// an in-kernel cross-workgroup handshake needs an agent-scope release, which
+// writes back the XCD's L2 -- far too slow for a few-microsecond block -- so
+// every dependency here is a kernel boundary and nothing inside a kernel
+// waits on another workgroup:
 //
-// 1. router_topk: the router matrix is split over many workgroups (one wave
-//    per expert, all tokens of the batch per wave, so R is read once), logits
-//    go to the workspace, and the last workgroup to finish (device-scope
-//    counter, self-resetting) runs top-k + softmax for every token with
-//    wave64 argmax butterflies. Strictly-greater-wins with an ascending scan
-//    is reproduced exactly: ties go to the lowest expert index.
-// 2. gate_up_swiglu: grid = (16-row tile, unique expert). Each workgroup
-//    derives the ascending list of distinct selected experts from idx, takes
-//    the u-th, and reads that expert's gate/up rows once for every token
-//    slot that selected it. A half-wave (32 lanes) owns one projection row
-//    (K = 2880 = 90 chunks -> 3 per lane), the other half the matching row of
-//    the other projection, so gate and up meet in registers for SwiGLU.
-// 3. down_combine: grid = (16-row tile, unique expert) again; per-slot
-//    partial outputs wgt*(down.h + bias) go to the workspace and the last
-//    workgroup of each row tile sums them in slot order (deterministic).
+// 1. moe_logits_k: router logits, one wave per expert reading its router row
+//    once for all tokens (fp32 accumulate), to the workspace; also half(x)
+//    when x is fp32 (router_topk writes xh the same way).
+// 2. moe_select_k (standalone router only): top-k + softmax per token.
+// 3. moe_gate_up_k: grid (16-row tile, u). Each workgroup derives the
+//    ascending list of distinct selected experts, takes the u-th and reads
+//    its gate/up rows once for every token slot that chose it. In the fused
+//    block each workgroup first runs top-k itself from the logits (a few
+//    hundred instructions, cheaper than a launch); workgroup (0,0) publishes
+//    idx/wgt. A half-wave (32 lanes) owns a gate row, the other half the
+//    matching up row (K = 2880 = 90 chunks -> 3 per lane), so SwiGLU happens
+//    on the two half-wave sums.
+// 4. moe_down_k: grid (8-row tile). A workgroup covers its rows for all
+//    selected experts (one wave per expert, looping), keeps per-slot
+//    wgt*(down.h + bias) in LDS and sums them in slot order: deterministic,
+//    no atomics.
 //
-// Weight rows are dequantised with the AND-OR fp16 trick of kq_device.h and
-// dotted against LDS-staged permuted activation pairs; the bf16 group scale
-// and bias are applied once per 32-weight chunk.
+// The activation a wave multiplies (x or h, per token slot) sits in its
+// registers as permuted fp16 pairs for all of the wave's rows; the weights
+// are dequantised with the AND-OR trick of kq_device.h; bf16 group scale and
+// bias apply once per 32-weight chunk.
 #include "kq_device.h"
 #include "kq_internal.h"
 
@@ -32,28 +37,27 @@ namespace kq {
 
 namespace {
 
-constexpr int kMoeThreads = 256;
-constexpr int kTileRows = 16;    // rows per workgroup (4 waves x 4 rows)
-constexpr int kSlotRound = 4;    // token slots staged per LDS round
+constexpr int kThreads = 256;
+constexpr int kGuRows = 16;   // gate/up rows per workgroup (4 waves x 4 rows)
+constexpr int kGuRW = 4;      // gate/up rows per wave
+constexpr int kDnRows = 8;    // down rows per workgroup
+constexpr int kMaxSlots = 128;
+constexpr int kMaxTopK = 8;
 
 struct WsLayout {
-    size_t cnt_router, cnt_tiles, lg, ys, total;
+    size_t lg, total;
 };
 
 WsLayout ws_layout(const kq_moe_desc& d, uint32_t batch) {
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
     WsLayout L;
-    const size_t ntiles = (d.hidden + kTileRows - 1) / kTileRows;
-    L.cnt_router = 0;
-    L.cnt_tiles = 64;
-    L.lg = al(L.cnt_tiles + 4 * ntiles);
-    L.ys = al(L.lg + 4ull * batch * d.n_experts);
-    L.total = al(L.ys + 4ull * batch * d.top_k * d.hidden);
+    L.lg = 0;
+    L.total = al(L.lg + 4ull * batch * d.n_experts);
     return L;
 }
 
 // ---------------------------------------------------------------------------
-// 1. router + top-k + softmax
+// 1. router logits
 // ---------------------------------------------------------------------------
 template <bool F32>
 __device__ __forceinline__ void load8(const void* p, size_t i, float v[8]) {
@@ -69,9 +73,55 @@ __device__ __forceinline__ void load8(const void* p, size_t i, float v[8]) {
     }
 }
 
-// (value, index) argmax with the reference's selection rule: a candidate is
-// selectable only if strictly greater than -inf (NaN never is); among equal
-// values the lower index wins.
+template <bool RF32, bool XF32>
+__global__ __launch_bounds__(kThreads) void moe_logits_k(const void* __restrict__ R,
+                                                         const void* __restrict__ X,
+                                                         uint32_t batch, uint32_t NE,
+                                                         uint32_t HID, uint16_t* __restrict__ xh,
+                                                         float* __restrict__ lg) {
+    constexpr int NBMAX = 16;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const uint32_t e = blockIdx.x * (kThreads / 64) + (tid >> 6);
+
+    if (XF32 && xh) {  // fp16 copy of x for the projections
+        const uint32_t tot = batch * HID;
+        for (uint32_t i = blockIdx.x * kThreads + tid; i < tot; i += gridDim.x * kThreads)
+            xh[i] = f2h(reinterpret_cast<const float*>(X)[i]);
+    }
+    if (e >= NE) return;
+    float acc[NBMAX];
+#pragma unroll
+    for (int t = 0; t < NBMAX; ++t) acc[t] = 0.0f;
+    for (uint32_t k = lane * 8; k < HID; k += 64 * 8) {
+        float r[8];
+        load8<RF32>(R, (size_t)e * HID + k, r);
+#pragma unroll
+        for (int t = 0; t < NBMAX; ++t) {
+            if ((uint32_t)t < batch) {
+                float x[8];
+                load8<XF32>(X, (size_t)t * HID + k, x);
+                float a = acc[t];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a = fmaf(r[i], x[i], a);
+                acc[t] = a;
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NBMAX; ++t) {
+        if ((uint32_t)t < batch) {
+            const float v = wave_sum(acc[t]);
+            if (lane == 0) lg[(size_t)t * NE + e] = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// top-k + softmax of one token, one wave (moe-fused/src/kernels.metal:149-162):
+// k passes of "strictly greater wins, ascending scan" -- ties go to the
+// lowest index, NaN and -inf are never selectable, and a pass with nothing
+// selectable picks expert 0 -- then softmax over the chosen logits.
+// ---------------------------------------------------------------------------
 __device__ __forceinline__ bool better(float va, uint32_t ia, float vb, uint32_t ib) {
     const bool oka = va > -INFINITY, okb = vb > -INFINITY;
     if (oka != okb) return oka;
@@ -79,75 +129,22 @@ __device__ __forceinline__ bool better(float va, uint32_t ia, float vb, uint32_t
     return va > vb || (va == vb && ia < ib);
 }
 
-template <bool RF32, bool XF32>
-__global__ __launch_bounds__(128) void moe_router_k(const void* __restrict__ R,
-                                                    const void* __restrict__ X, uint32_t batch,
-                                                    uint32_t NE, uint32_t HID, uint32_t TK,
-                                                    uint32_t* __restrict__ idx,
-                                                    float* __restrict__ wgt,
-                                                    uint16_t* __restrict__ xh,
-                                                    float* __restrict__ lg,
-                                                    uint32_t* __restrict__ counter) {
-    constexpr int NBMAX = 16;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t e = blockIdx.x * 2 + wave;
-
-    // fp16 copy of x for the projections (router_topk writes xh the same way,
-    // moe-fused/src/kernels.metal:137)
-    if (XF32 && xh) {
-        const uint32_t tot = batch * HID;
-        for (uint32_t i = blockIdx.x * 128 + tid; i < tot; i += gridDim.x * 128)
-            xh[i] = f2h(reinterpret_cast<const float*>(X)[i]);
+__device__ void topk_wave(const float* __restrict__ L, uint32_t NE, uint32_t TK,
+                          uint32_t* idx_out, float* wgt_out) {
+    const uint32_t lane = threadIdx.x & 63;
+    float v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t ei = lane + 64 * q;
+        v[q] = ei < NE ? L[ei] : -INFINITY;
     }
-
-    if (e < NE) {
-        float acc[NBMAX];
+    float chosen[kMaxTopK];
+    uint32_t pick[kMaxTopK];
 #pragma unroll
-        for (int t = 0; t < NBMAX; ++t) acc[t] = 0.0f;
-        for (uint32_t k = lane * 8; k < HID; k += 64 * 8) {
-            float r[8];
-            load8<RF32>(R, (size_t)e * HID + k, r);
-#pragma unroll
-            for (int t = 0; t < NBMAX; ++t) {
-                if ((uint32_t)t < batch) {
-                    float x[8];
-                    load8<XF32>(X, (size_t)t * HID + k, x);
-                    float a = acc[t];
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) a = fmaf(r[i], x[i], a);
-                    acc[t] = a;
-                }
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < NBMAX; ++t) {
-            if ((uint32_t)t < batch) {
-                const float v = wave_sum(acc[t]);
-                if (lane == 0) lg[(size_t)t * NE + e] = v;
-            }
-        }
-    }
-
-    // last-workgroup-done epilogue
-    __shared__ uint32_t s_last;
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(counter, 1u) == gridDim.x - 1);
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-
-    for (uint32_t t = wave; t < batch; t += 2) {
-        const volatile float* L = lg + (size_t)t * NE;
-        float v[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t ei = lane + 64 * q;
-            v[q] = ei < NE ? L[ei] : -INFINITY;
-        }
-        float chosen[8];
-        uint32_t pick[8];
-        for (uint32_t j = 0; j < TK; ++j) {
+    for (int j = 0; j < kMaxTopK; ++j) {
+        chosen[j] = -INFINITY;
+        pick[j] = 0;
+        if ((uint32_t)j < TK) {
             float bv = -INFINITY;
             uint32_t bi = 0xFFFFFFFFu;
 #pragma unroll
@@ -161,39 +158,46 @@ __global__ __launch_bounds__(128) void moe_router_k(const void* __restrict__ R,
                 const uint32_t oi = __shfl_xor(bi, o, 64);
                 if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
             }
-            if (!(bv > -INFINITY)) { bv = -INFINITY; bi = 0; }  // nothing selectable
+            if (!(bv > -INFINITY)) { bv = -INFINITY; bi = 0; }
             chosen[j] = bv;
             pick[j] = bi;
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                if ((uint32_t)lane + 64 * q == bi) v[q] = -INFINITY;
-        }
-        if (lane == 0) {
-            float mx = chosen[0];
-            for (uint32_t j = 1; j < TK; ++j) mx = fmaxf(mx, chosen[j]);
-            float sum = 0.0f, ex[8];
-            for (uint32_t j = 0; j < TK; ++j) { ex[j] = expf(chosen[j] - mx); sum += ex[j]; }
-            for (uint32_t j = 0; j < TK; ++j) {
-                idx[t * TK + j] = pick[j];
-                wgt[t * TK + j] = ex[j] / sum;
-            }
+                if (lane + 64 * q == bi) v[q] = -INFINITY;
         }
     }
-    if (tid == 0) atomicExch(counter, 0u);
+    if (lane == 0) {
+        float mx = chosen[0];
+#pragma unroll
+        for (int j = 1; j < kMaxTopK; ++j)
+            if ((uint32_t)j < TK) mx = fmaxf(mx, chosen[j]);
+        float ex[kMaxTopK], sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMaxTopK; ++j) {
+            ex[j] = 0.0f;
+            if ((uint32_t)j < TK) { ex[j] = expf(chosen[j] - mx); sum += ex[j]; }
+        }
+#pragma unroll
+        for (int j = 0; j < kMaxTopK; ++j)
+            if ((uint32_t)j < TK) { idx_out[j] = pick[j]; wgt_out[j] = ex[j] / sum; }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void moe_select_k(const float* __restrict__ lg,
+                                                         uint32_t batch, uint32_t NE,
+                                                         uint32_t TK, uint32_t* __restrict__ idx,
+                                                         float* __restrict__ wgt) {
+    for (uint32_t t = threadIdx.x >> 6; t < batch; t += kThreads / 64)
+        topk_wave(lg + (size_t)t * NE, NE, TK, idx + t * TK, wgt + t * TK);
 }
 
 // ---------------------------------------------------------------------------
-// shared by passes 2 and 3: the expert of work item u and its token slots
+// Which expert a work item handles, and its token slots
 // ---------------------------------------------------------------------------
-struct Plan {
-    uint32_t e;         // expert id (valid if u < n_unique)
-    uint32_t n_unique;  // distinct experts selected
-    uint64_t m0, m1;    // slots s (s < 64: bit s of m0; else bit s-64 of m1)
-};
-
-__device__ Plan moe_plan(const uint32_t* __restrict__ idx, uint32_t nslots, uint32_t NE,
-                         uint32_t u, uint32_t* bits /* LDS, 8 words */) {
-    const int tid = threadIdx.x, lane = tid & 63;
+// Marks the experts selected by the slots in an LDS bitmap of 8 words.
+__device__ __forceinline__ void mark_experts(const uint32_t* idx, uint32_t nslots, uint32_t NE,
+                                             uint32_t* bits) {
+    const int tid = threadIdx.x;
     if (tid < 8) bits[tid] = 0;
     __syncthreads();
     if ((uint32_t)tid < nslots) {
@@ -201,6 +205,19 @@ __device__ Plan moe_plan(const uint32_t* __restrict__ idx, uint32_t nslots, uint
         atomicOr(&bits[e >> 5], 1u << (e & 31));
     }
     __syncthreads();
+}
+
+struct Plan {
+    uint32_t e;         // expert id (valid if u < n_unique)
+    uint32_t n_unique;  // distinct experts selected
+    uint64_t m0, m1;    // slots s (s < 64: bit s of m0; else bit s-64 of m1)
+};
+
+// The u-th smallest marked expert and the slots that selected it (wave-level;
+// every lane of the wave must be active).
+__device__ Plan plan_for(const uint32_t* idx, uint32_t nslots, uint32_t NE, uint32_t u,
+                         const uint32_t* bits) {
+    const uint32_t lane = threadIdx.x & 63;
     Plan p;
     p.e = 0xFFFFFFFFu;
     uint32_t cnt = 0;
@@ -215,9 +232,8 @@ __device__ Plan moe_plan(const uint32_t* __restrict__ idx, uint32_t nslots, uint
         cnt += pc;
     }
     p.n_unique = cnt;
-    const uint32_t s0 = lane, s1 = lane + 64;
-    const bool q0 = s0 < nslots && min(idx[s0], NE - 1) == p.e;
-    const bool q1 = s1 < nslots && min(idx[s1], NE - 1) == p.e;
+    const bool q0 = lane < nslots && min(idx[lane], NE - 1) == p.e;
+    const bool q1 = lane + 64 < nslots && min(idx[lane + 64], NE - 1) == p.e;
     p.m0 = __ballot(q0);
     p.m1 = __ballot(q1);
     return p;
@@ -230,58 +246,47 @@ __device__ __forceinline__ uint32_t pop_slot(uint64_t& m0, uint64_t& m1) {
     return s;
 }
 
-// Stage activation vectors (fp16 [K]) of up to kSlotRound slots into LDS as
-// permuted pairs [slot][word%4][chunk] and per-chunk (sum, offset const).
-__device__ __forceinline__ void stage_acts(const uint16_t* base, const uint32_t* offs, int ns,
-                                           uint32_t K, u32x4* xp, float2* xk) {
-    const uint32_t nw = K >> 3, nch = K >> 5;
-    const uint32_t total = (uint32_t)ns * nw;
-    const int tid = threadIdx.x;
-    for (uint32_t w0 = 0; w0 < total; w0 += kMoeThreads) {
-        const uint32_t w = w0 + tid;
-        const bool ok = w < total;
-        const uint32_t t = ok ? w / nw : 0, wi = ok ? w - t * nw : 0;
-        u32x4 v = ok ? *reinterpret_cast<const u32x4*>(base + (size_t)offs[t] + (size_t)wi * 8)
-                     : u32x4{0, 0, 0, 0};
-        float s, c;
-        word_consts(v, s, c);
-        s = group_sum<4>(s);
-        c = group_sum<4>(c);
-        if (ok) {
-            const uint32_t ch = wi >> 2, j = wi & 3;
-            xp[(t * 4 + j) * nch + ch] = pair_perm(v);
-            if (j == 0) xk[t * nch + ch] = make_float2(s, c);
-        }
-    }
-}
-
-// Partial (per-lane) dot of J chunks of one row with staged activation slot t.
+// ---------------------------------------------------------------------------
+// register-resident activation: chunks c0 + 32j (j < J) of one fp16 vector
+// ---------------------------------------------------------------------------
 template <int J>
-__device__ __forceinline__ float row_partial(const u32x4 (&w)[J], const uint32_t (&mt)[J],
-                                             const u32x4* xp, const float2* xk, uint32_t t,
-                                             uint32_t nch, uint32_t c0) {
-    float acc = 0.0f;
+struct Act {
+    u32x4 p[J][4];   // permuted pairs of the chunk's 4 words
+    float xs[J];     // chunk sum
+    float xc[J];     // chunk offset constant
+};
+
+template <int J>
+__device__ __forceinline__ void act_load(const uint16_t* __restrict__ v, uint32_t nch, uint32_t c0,
+                                         u32x4 (&raw)[J][4]) {
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const uint32_t c = c0 + 32 * j;
-        if (c < nch) {
-            const u32x4 p0 = xp[(t * 4 + 0) * nch + c];
-            const u32x4 p1 = xp[(t * 4 + 1) * nch + c];
-            const u32x4 p2 = xp[(t * 4 + 2) * nch + c];
-            const u32x4 p3 = xp[(t * 4 + 3) * nch + c];
-            const float2 k2 = xk[t * nch + c];
-            float da = qdot8(w[j].x, p0, 0.0f);
-            float db = qdot8(w[j].y, p1, 0.0f);
-            da = qdot8(w[j].z, p2, da);
-            db = qdot8(w[j].w, p3, db);
-            const float s = bf2f(mt[j] & 0xFFFFu), b = bf2f(mt[j] >> 16);
-            acc = fmaf(s, (da + db) - k2.y, fmaf(b, k2.x, acc));
-        }
+        const uint32_t c = min(c0 + 32 * j, nch - 1);
+        const u32x4* src = reinterpret_cast<const u32x4*>(v) + (size_t)c * 4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) raw[j][q] = src[q];
     }
-    return acc;
 }
 
-// Load J chunks (lane c0 + 32j) of row m of a projection plus bf16 S/B.
+template <int J>
+__device__ __forceinline__ void act_prep(const u32x4 (&raw)[J][4], Act<J>& a) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        float s = 0.0f, c = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float ws, wc;
+            word_consts(raw[j][q], ws, wc);
+            s += ws;
+            c += wc;
+            a.p[j][q] = pair_perm(raw[j][q]);
+        }
+        a.xs[j] = s;
+        a.xc[j] = c;
+    }
+}
+
+// Load J chunks (lane c0 + 32j) of row m of a projection plus bf16 S|B.
 template <int J>
 __device__ __forceinline__ void load_row(const uint8_t* proj, const kq_moe_desc& d, uint32_t K,
                                          uint32_t m, uint32_t c0, u32x4 (&w)[J],
@@ -298,154 +303,223 @@ __device__ __forceinline__ void load_row(const uint8_t* proj, const kq_moe_desc&
     }
 }
 
-// ---------------------------------------------------------------------------
-// 2. gather + gate + up + SwiGLU
-// ---------------------------------------------------------------------------
+// Per-lane partial dot of one row's J chunks with a register activation.
 template <int J>
-__global__ __launch_bounds__(kMoeThreads) void moe_gate_up_k(
-    const uint8_t* __restrict__ pool, kq_moe_desc d, const uint32_t* __restrict__ idx,
+__device__ __forceinline__ float row_dot(const u32x4 (&w)[J], const uint32_t (&mt)[J],
+                                         const Act<J>& a, uint32_t nch, uint32_t c0,
+                                         const DequantConsts& kc) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        if (c0 + 32 * j < nch) {
+            float da = qdot8(w[j].x, a.p[j][0], 0.0f, kc);
+            float db = qdot8(w[j].y, a.p[j][1], 0.0f, kc);
+            da = qdot8(w[j].z, a.p[j][2], da, kc);
+            db = qdot8(w[j].w, a.p[j][3], db, kc);
+            const float s = bf2f(mt[j] & 0xFFFFu), b = bf2f(mt[j] >> 16);
+            acc = fmaf(s, (da + db) - a.xc[j], fmaf(b, a.xs[j], acc));
+        }
+    }
+    return acc;
+}
+
+// ---------------------------------------------------------------------------
+// 3. gather + gate + up + SwiGLU
+// ---------------------------------------------------------------------------
+template <int J, bool FROM_LOGITS>
+__global__ __launch_bounds__(kThreads) void moe_gate_up_k(
+    const uint8_t* __restrict__ pool, kq_moe_desc d, const uint32_t* __restrict__ idx_g,
+    float* __restrict__ wgt_pub, uint32_t* __restrict__ idx_pub, const float* __restrict__ lg,
     const uint16_t* __restrict__ xh, uint16_t* __restrict__ H, uint32_t batch) {
-    extern __shared__ __align__(16) unsigned char smem[];
     __shared__ uint32_t bits[8];
+    __shared__ uint32_t s_idx[kMaxSlots];
+    __shared__ float s_wgt[kMaxSlots];
     const uint32_t HID = d.hidden, IN = d.inter, TK = d.top_k;
     const uint32_t nslots = batch * TK;
-    const Plan p = moe_plan(idx, nslots, d.n_experts, blockIdx.y, bits);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    const uint32_t* idx = idx_g;
+    if constexpr (FROM_LOGITS) {
+        for (uint32_t t = wave; t < batch; t += kThreads / 64)
+            topk_wave(lg + (size_t)t * d.n_experts, d.n_experts, TK, s_idx + t * TK,
+                      s_wgt + t * TK);
+        __syncthreads();
+        if (blockIdx.x == 0 && blockIdx.y == 0 && (uint32_t)tid < nslots) {
+            idx_pub[tid] = s_idx[tid];  // for the down pass and the caller
+            wgt_pub[tid] = s_wgt[tid];
+        }
+        idx = s_idx;
+    }
+    mark_experts(idx, nslots, d.n_experts, bits);
+    const Plan p = plan_for(idx, nslots, d.n_experts, blockIdx.y, bits);
     if (blockIdx.y >= p.n_unique) return;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t half = lane >> 5, c0 = lane & 31, nch = HID >> 5;
     const uint8_t* blob = pool + (size_t)p.e * d.blob;
     const uint8_t* proj = blob + (half ? d.off_up : d.off_gate);
+    const uint32_t m0 = blockIdx.x * kGuRows + wave * kGuRW;
+    const DequantConsts kc;
 
-    // issue this wave's weight loads before staging activations
-    constexpr int RW = kTileRows / 4;  // rows per wave
-    const uint32_t mrow0 = blockIdx.x * kTileRows + wave * RW;
-    u32x4 w[RW][J];
-    uint32_t mt[RW][J];
-    float bias[RW];
+    uint64_t sm0 = p.m0, sm1 = p.m1;
+    uint32_t slot = pop_slot(sm0, sm1);
+    // x of the first slot ahead of the weights in the memory queue
+    u32x4 raw[J][4];
+    act_load<J>(xh + (size_t)(slot / TK) * HID, nch, c0, raw);
+
+    u32x4 w[kGuRW][J];
+    uint32_t mt[kGuRW][J];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-        const uint32_t m = min(mrow0 + r, IN - 1);
-        load_row<J>(proj, d, HID, m, c0, w[r], mt[r]);
-        bias[r] = bf2f(reinterpret_cast<const uint16_t*>(proj + d.sub_bi)[m]);
+    for (int r = 0; r < kGuRW; ++r) load_row<J>(proj, d, HID, min(m0 + r, IN - 1), c0, w[r], mt[r]);
+    float bg = 0.0f, bu = 0.0f;
+    if (lane < kGuRW && m0 + lane < IN) {
+        bg = bf2f(reinterpret_cast<const uint16_t*>(blob + d.off_gate + d.sub_bi)[m0 + lane]);
+        bu = bf2f(reinterpret_cast<const uint16_t*>(blob + d.off_up + d.sub_bi)[m0 + lane]);
     }
 
-    u32x4* xp = reinterpret_cast<u32x4*>(smem);
-    float2* xk = reinterpret_cast<float2*>(smem + (size_t)kSlotRound * nch * 64);
-    __shared__ uint32_t s_sl[kSlotRound], s_off[kSlotRound];
-    uint64_t m0 = p.m0, m1 = p.m1;
-    while (m0 | m1) {
-        __syncthreads();  // previous round's LDS reads are done
-        int ns = 0;
-        while ((m0 | m1) && ns < kSlotRound) {
-            const uint32_t sl = pop_slot(m0, m1);
-            if (tid == 0) { s_sl[ns] = sl; s_off[ns] = (sl / TK) * HID; }
-            ++ns;
-        }
-        __syncthreads();
-        stage_acts(xh, s_off, ns, HID, xp, xk);
-        __syncthreads();
-        for (int t = 0; t < ns; ++t) {
-            const uint32_t slot = s_sl[t];
+    while (true) {
+        Act<J> a;
+        act_prep<J>(raw, a);
+        float g[kGuRW], u[kGuRW];
 #pragma unroll
-            for (int r = 0; r < RW; ++r) {
-                float v = group_sum<32>(row_partial<J>(w[r], mt[r], xp, xk, t, nch, c0)) + bias[r];
-                const float o = __shfl_xor(v, 32, 64);
-                const uint32_t m = mrow0 + r;
-                if (lane == r && m < IN) {
-                    const float g = fminf(v, 7.0f);  // lane < 32 holds gate
-                    const float uu = fminf(fmaxf(o, -7.0f), 7.0f);
-                    const float h = (g / (1.0f + expf(-1.702f * g))) * (uu + 1.0f);
-                    H[(size_t)slot * IN + m] = f2h(h);
-                }
+        for (int r = 0; r < kGuRW; ++r) {
+            const float2 hs = half_sums(row_dot<J>(w[r], mt[r], a, nch, c0, kc));
+            g[r] = hs.x;
+            u[r] = hs.y;
+        }
+#pragma unroll
+        for (int r = 0; r < kGuRW; ++r) {
+            if (lane == r && m0 + r < IN) {
+                const float gg = fminf(g[r] + bg, 7.0f);
+                const float uu = fminf(fmaxf(u[r] + bu, -7.0f), 7.0f);
+                const float h = (gg / (1.0f + expf(-1.702f * gg))) * (uu + 1.0f);
+                H[(size_t)slot * IN + m0 + r] = f2h(h);
             }
         }
+        if (!(sm0 | sm1)) break;
+        slot = pop_slot(sm0, sm1);
+        act_load<J>(xh + (size_t)(slot / TK) * HID, nch, c0, raw);
     }
 }
 
 // ---------------------------------------------------------------------------
-// 3. gather + down + weighted combine
+// 4. gather + down + weighted combine
 // ---------------------------------------------------------------------------
 template <int J>
-__global__ __launch_bounds__(kMoeThreads) void moe_down_k(
+__global__ __launch_bounds__(kThreads) void moe_down_k(
     const uint8_t* __restrict__ pool, kq_moe_desc d, const uint32_t* __restrict__ idx,
     const float* __restrict__ wgt, const uint16_t* __restrict__ H, void* __restrict__ Y,
-    int y_f32, uint32_t batch, float* __restrict__ ys, uint32_t* __restrict__ tile_cnt) {
-    extern __shared__ __align__(16) unsigned char smem[];
+    int y_f32, uint32_t batch) {
     __shared__ uint32_t bits[8];
-    __shared__ uint32_t s_last;
+    __shared__ uint32_t s_idx[kMaxSlots];
+    __shared__ float s_wgt[kMaxSlots];
+    __shared__ float ys[kMaxSlots][kDnRows];
     const uint32_t HID = d.hidden, IN = d.inter, TK = d.top_k;
     const uint32_t nslots = batch * TK;
-    const Plan p = moe_plan(idx, nslots, d.n_experts, blockIdx.y, bits);
-    if (blockIdx.y >= p.n_unique) return;
-
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t half = lane >> 5, c0 = lane & 31, nch = IN >> 5;
-    const uint8_t* proj = pool + (size_t)p.e * d.blob + d.off_down;
-
-    // wave rows: pairs (2q, 2q+1), the half-wave picks one of the pair
-    constexpr int RP = kTileRows / 8;  // row pairs per wave
-    const uint32_t mrow0 = blockIdx.x * kTileRows + wave * (2 * RP);
-    u32x4 w[RP][J];
-    uint32_t mt[RP][J];
-    float bias[RP];
-#pragma unroll
-    for (int r = 0; r < RP; ++r) {
-        const uint32_t m = min(mrow0 + 2 * r + half, HID - 1);
-        load_row<J>(proj, d, IN, m, c0, w[r], mt[r]);
-        bias[r] = bf2f(reinterpret_cast<const uint16_t*>(proj + d.sub_bi)[m]);
+    if ((uint32_t)tid < nslots) {
+        s_idx[tid] = idx[tid];
+        s_wgt[tid] = wgt[tid];
     }
+    mark_experts(s_idx, nslots, d.n_experts, bits);  // (its first barrier publishes s_idx)
+    const uint32_t half = lane >> 5, c0 = lane & 31, nch = IN >> 5;
+    const uint32_t m0 = blockIdx.x * kDnRows;
+    constexpr int RP = kDnRows / 2;  // row pairs per wave
+    const DequantConsts kc;
+    uint32_t n_unique = 0;
+#pragma unroll
+    for (int wd = 0; wd < 8; ++wd) n_unique += __popc(bits[wd]);
 
-    u32x4* xp = reinterpret_cast<u32x4*>(smem);
-    float2* xk = reinterpret_cast<float2*>(smem + (size_t)kSlotRound * nch * 64);
-    __shared__ uint32_t s_sl[kSlotRound], s_off[kSlotRound];
-    uint64_t m0 = p.m0, m1 = p.m1;
-    while (m0 | m1) {
-        __syncthreads();
-        int ns = 0;
-        while ((m0 | m1) && ns < kSlotRound) {
-            const uint32_t sl = pop_slot(m0, m1);
-            if (tid == 0) { s_sl[ns] = sl; s_off[ns] = sl * IN; }
-            ++ns;
+    // the distinct experts, one wave each (looping when there are more)
+    for (uint32_t u = wave; u < n_unique; u += kThreads / 64) {
+        const Plan p = plan_for(s_idx, nslots, d.n_experts, u, bits);
+        const uint8_t* proj = pool + (size_t)p.e * d.blob + d.off_down;
+        uint64_t sm0 = p.m0, sm1 = p.m1;
+        uint32_t slot = pop_slot(sm0, sm1);
+        u32x4 raw[J][4];
+        act_load<J>(H + (size_t)slot * IN, nch, c0, raw);
+        u32x4 w[RP][J];
+        uint32_t mt[RP][J];
+#pragma unroll
+        for (int r = 0; r < RP; ++r)
+            load_row<J>(proj, d, IN, min(m0 + 2 * r + half, HID - 1), c0, w[r], mt[r]);
+        float bi0 = 0.0f, bi1 = 0.0f;
+        if (lane < RP) {
+            const uint16_t* BI = reinterpret_cast<const uint16_t*>(proj + d.sub_bi);
+            bi0 = bf2f(BI[min(m0 + 2 * lane, HID - 1)]);
+            bi1 = bf2f(BI[min(m0 + 2 * lane + 1, HID - 1)]);
         }
-        __syncthreads();
-        stage_acts(H, s_off, ns, IN, xp, xk);
-        __syncthreads();
-        for (int t = 0; t < ns; ++t) {
-            const uint32_t slot = s_sl[t];
-            const float wt = wgt[slot];
+        while (true) {
+            Act<J> a;
+            act_prep<J>(raw, a);
+            const float wt = s_wgt[slot];
+            float2 hs[RP];
+#pragma unroll
+            for (int r = 0; r < RP; ++r) hs[r] = half_sums(row_dot<J>(w[r], mt[r], a, nch, c0, kc));
 #pragma unroll
             for (int r = 0; r < RP; ++r) {
-                const float v = group_sum<32>(row_partial<J>(w[r], mt[r], xp, xk, t, nch, c0));
-                const uint32_t m = mrow0 + 2 * r + half;
-                if (c0 == 0 && m < HID) ys[(size_t)slot * HID + m] = wt * (v + bias[r]);
+                if (lane == r) {
+                    ys[slot][2 * r] = wt * (hs[r].x + bi0);
+                    ys[slot][2 * r + 1] = wt * (hs[r].y + bi1);
+                }
             }
+            if (!(sm0 | sm1)) break;
+            slot = pop_slot(sm0, sm1);
+            act_load<J>(H + (size_t)slot * IN, nch, c0, raw);
         }
     }
-
-    // the last of the n_unique workgroups of this row tile combines in slot order
-    __threadfence();
     __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(&tile_cnt[blockIdx.x], 1u) == p.n_unique - 1);
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const uint32_t mt0 = blockIdx.x * kTileRows;
-    for (uint32_t i = tid; i < batch * kTileRows; i += kMoeThreads) {
-        const uint32_t t = i / kTileRows, m = mt0 + i % kTileRows;
+    // combine in slot order (moe-fused/src/kernels.metal:254-263)
+    for (uint32_t i = tid; i < batch * kDnRows; i += kThreads) {
+        const uint32_t t = i / kDnRows, r = i % kDnRows, m = m0 + r;
         if (m >= HID) continue;
-        const volatile float* yv = ys + (size_t)t * TK * HID + m;
         float acc = 0.0f;
-        for (uint32_t k = 0; k < TK; ++k) acc += yv[(size_t)k * HID];
+        for (uint32_t k = 0; k < TK; ++k) acc += ys[t * TK + k][r];
         if (y_f32) reinterpret_cast<float*>(Y)[(size_t)t * HID + m] = acc;
         else reinterpret_cast<uint16_t*>(Y)[(size_t)t * HID + m] = f2h(acc);
     }
-    if (tid == 0) atomicExch(&tile_cnt[blockIdx.x], 0u);
 }
 
 __global__ void fill_zero_k(uint32_t* p, size_t n) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
         p[i] = 0u;
+}
+
+uint32_t max_unique(const kq_moe_desc& d, uint32_t batch) {
+    const uint32_t n = batch * d.top_k;
+    return n < d.n_experts ? n : d.n_experts;
+}
+
+uint32_t chunks_j(uint32_t K) { return ((K >> 5) + 31) / 32; }
+
+hipError_t launch_logits(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
+                         const kq_moe_desc& d, uint16_t* xh, float* lg, hipStream_t s) {
+    const dim3 grid((d.n_experts + 3) / 4);
+#define KQ_LG(RF, XF)                                                                           \
+    moe_logits_k<RF, XF><<<grid, kThreads, 0, s>>>(R, X, batch, d.n_experts, d.hidden, xh, lg)
+    if (r_f32 && x_f32) KQ_LG(true, true);
+    else if (r_f32) KQ_LG(true, false);
+    else if (x_f32) KQ_LG(false, true);
+    else KQ_LG(false, false);
+#undef KQ_LG
+    return hipGetLastError();
+}
+
+template <bool FL>
+hipError_t launch_gu(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx, float* wgt,
+                     uint32_t* idx_pub, const float* lg, const uint16_t* xh, uint16_t* H,
+                     uint32_t batch, hipStream_t s) {
+    const dim3 grid((d.inter + kGuRows - 1) / kGuRows, max_unique(d, batch));
+#define KQ_GU(JJ)                                                                               \
+    moe_gate_up_k<JJ, FL><<<grid, kThreads, 0, s>>>(pool, d, idx, wgt, idx_pub, lg, xh, H, batch)
+    switch (chunks_j(d.hidden)) {
+        case 1: KQ_GU(1); break;
+        case 2: KQ_GU(2); break;
+        case 3: KQ_GU(3); break;
+        case 4: KQ_GU(4); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef KQ_GU
+    return hipGetLastError();
 }
 
 }  // namespace
@@ -464,61 +538,46 @@ hipError_t launch_ws_zero(void* ws, size_t bytes, hipStream_t s) {
 hipError_t launch_moe_router(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
                              const kq_moe_desc& d, uint32_t* idx, float* wgt, uint16_t* xh,
                              void* ws, hipStream_t s) {
-    const WsLayout L = ws_layout(d, batch);
-    uint8_t* w = reinterpret_cast<uint8_t*>(ws);
-    float* lg = reinterpret_cast<float*>(w + L.lg);
-    uint32_t* cnt = reinterpret_cast<uint32_t*>(w + L.cnt_router);
-    const dim3 grid((d.n_experts + 1) / 2);
-#define KQ_ROUTER(RF, XF)                                                                       \
-    moe_router_k<RF, XF><<<grid, 128, 0, s>>>(R, X, batch, d.n_experts, d.hidden, d.top_k, idx, \
-                                              wgt, xh, lg, cnt)
-    if (r_f32 && x_f32) KQ_ROUTER(true, true);
-    else if (r_f32) KQ_ROUTER(true, false);
-    else if (x_f32) KQ_ROUTER(false, true);
-    else KQ_ROUTER(false, false);
-#undef KQ_ROUTER
+    float* lg = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + ws_layout(d, batch).lg);
+    hipError_t e = launch_logits(R, r_f32, X, x_f32, batch, d, xh, lg, s);
+    if (e != hipSuccess) return e;
+    moe_select_k<<<1, kThreads, 0, s>>>(lg, batch, d.n_experts, d.top_k, idx, wgt);
     return hipGetLastError();
-}
-
-static uint32_t max_unique(const kq_moe_desc& d, uint32_t batch) {
-    const uint32_t n = batch * d.top_k;
-    return n < d.n_experts ? n : d.n_experts;
 }
 
 hipError_t launch_moe_gate_up(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
                               const uint16_t* xh, uint16_t* H, uint32_t batch, hipStream_t s) {
-    const uint32_t J = ((d.hidden >> 5) + 31) / 32;
-    const dim3 grid((d.inter + kTileRows - 1) / kTileRows, max_unique(d, batch));
-    const size_t lds = (size_t)kSlotRound * (d.hidden >> 5) * 72;
-    switch (J) {
-        case 1: moe_gate_up_k<1><<<grid, kMoeThreads, lds, s>>>(pool, d, idx, xh, H, batch); break;
-        case 2: moe_gate_up_k<2><<<grid, kMoeThreads, lds, s>>>(pool, d, idx, xh, H, batch); break;
-        case 3: moe_gate_up_k<3><<<grid, kMoeThreads, lds, s>>>(pool, d, idx, xh, H, batch); break;
-        case 4: moe_gate_up_k<4><<<grid, kMoeThreads, lds, s>>>(pool, d, idx, xh, H, batch); break;
-        default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    return launch_gu<false>(pool, d, idx, nullptr, nullptr, nullptr, xh, H, batch, s);
 }
 
 hipError_t launch_moe_down(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
                            const float* wgt, const uint16_t* H, void* Y, bool y_f32,
-                           uint32_t batch, void* ws, hipStream_t s) {
-    const WsLayout L = ws_layout(d, batch);
-    uint8_t* w = reinterpret_cast<uint8_t*>(ws);
-    float* ys = reinterpret_cast<float*>(w + L.ys);
-    uint32_t* tc = reinterpret_cast<uint32_t*>(w + L.cnt_tiles);
-    const uint32_t J = ((d.inter >> 5) + 31) / 32;
-    const dim3 grid((d.hidden + kTileRows - 1) / kTileRows, max_unique(d, batch));
-    const size_t lds = (size_t)kSlotRound * (d.inter >> 5) * 72;
+                           uint32_t batch, hipStream_t s) {
+    const dim3 grid((d.hidden + kDnRows - 1) / kDnRows);
     const int yf = y_f32 ? 1 : 0;
-    switch (J) {
-        case 1: moe_down_k<1><<<grid, kMoeThreads, lds, s>>>(pool, d, idx, wgt, H, Y, yf, batch, ys, tc); break;
-        case 2: moe_down_k<2><<<grid, kMoeThreads, lds, s>>>(pool, d, idx, wgt, H, Y, yf, batch, ys, tc); break;
-        case 3: moe_down_k<3><<<grid, kMoeThreads, lds, s>>>(pool, d, idx, wgt, H, Y, yf, batch, ys, tc); break;
-        case 4: moe_down_k<4><<<grid, kMoeThreads, lds, s>>>(pool, d, idx, wgt, H, Y, yf, batch, ys, tc); break;
+#define KQ_DN(JJ) moe_down_k<JJ><<<grid, kThreads, 0, s>>>(pool, d, idx, wgt, H, Y, yf, batch)
+    switch (chunks_j(d.inter)) {
+        case 1: KQ_DN(1); break;
+        case 2: KQ_DN(2); break;
+        case 3: KQ_DN(3); break;
+        case 4: KQ_DN(4); break;
         default: return hipErrorInvalidValue;
     }
+#undef KQ_DN
     return hipGetLastError();
+}
+
+hipError_t launch_moe_block(const uint8_t* pool, const kq_moe_desc& d, const void* R, bool r_f32,
+                            const void* X, bool x_f32, uint32_t batch, uint32_t* idx, float* wgt,
+                            uint16_t* xh, uint16_t* H, void* Y, bool y_f32, void* ws,
+                            hipStream_t s) {
+    float* lg = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + ws_layout(d, batch).lg);
+    hipError_t e = launch_logits(R, r_f32, X, x_f32, batch, d, xh, lg, s);
+    if (e != hipSuccess) return e;
+    const uint16_t* xin = x_f32 ? xh : reinterpret_cast<const uint16_t*>(X);
+    e = launch_gu<true>(pool, d, nullptr, wgt, idx, lg, xin, H, batch, s);
+    if (e != hipSuccess) return e;
+    return launch_moe_down(pool, d, idx, wgt, H, Y, y_f32, batch, s);
 }
 
 }  // namespace kq

@@ -92,13 +92,21 @@ def test_batched_valu(gpu, batch):
     check(run_int4(p, gpu, path=kq.PATH_VALU), ref_int4(p), f"valu batch {batch}")
 
 
-@pytest.mark.parametrize("rows,unroll", [(1, 1), (1, 2), (1, 4), (1, 8), (2, 1), (2, 2), (2, 4),
-                                         (2, 8)])
-def test_forced_launch_shapes_agree(gpu, rows, unroll):
-    p = gen.int4_problem(1031, 8192, 64, seed=11)
-    ref = ref_int4(p)
+@pytest.mark.parametrize("rows,unroll", [(1, 1), (2, 1), (4, 1), (1, 2), (2, 2), (1, 4)])
+@pytest.mark.parametrize("K", [8192, 2880, 28672])
+def test_forced_launch_shapes_agree(gpu, rows, unroll, K):
+    """Every (rows per item, 64-chunk steps per item) shape gives the same
+    answer, including segment counts that do not divide the row."""
+    p = gen.int4_problem(1031, K, 64, seed=11 + K)
     got = run_int4(p, gpu, path=kq.PATH_VALU, rows=rows, unroll=unroll)
-    check(got, ref, f"rows={rows} unroll={unroll}")
+    check(got, ref_int4(p), f"rows={rows} unroll={unroll} K={K}")
+
+
+def test_forced_launch_shape_unsupported(gpu):
+    p = gen.int4_problem(64, 8192, 64, seed=1)
+    with pytest.raises(kq.KQError) as e:
+        run_int4(p, gpu, path=kq.PATH_VALU, rows=4, unroll=4)  # 16 loads per buffer: too many
+    assert e.value.status == kq.KQ_EUNSUPPORTED
 
 
 def test_deterministic(gpu):
@@ -125,3 +133,37 @@ def test_stream_read_runs(gpu):
     kq.stream_read(src, n, sink)
     torch.cuda.synchronize()
     assert sink.cpu().tolist() == [0, 0, 0, 0]  # fold of zeros is not all ones
+
+
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 8, 9, 16])
+@pytest.mark.parametrize("M,K,G", [(4096, 4096, 64), (1031, 14336, 64), (777, 2944, 64),
+                                   (300, 8192, 128), (64, 28672, 64), (33, 1152, 128)])
+def test_mfma_path(gpu, M, K, G, batch):
+    """Matrix-core path: split-K over 16 waves, rounds of 8 steps, LDS
+    reduction; batches past one LDS pass re-run over the token groups."""
+    p = gen.int4_problem(M, K, G, batch=batch, seed=M + K + G + batch)
+    check(run_int4(p, gpu, path=kq.PATH_MFMA), ref_int4(p), f"mfma M={M} K={K} G={G} b={batch}")
+
+
+@pytest.mark.parametrize("layout", ["sb", "split"])
+def test_mfma_layouts_bf16_fp32out(gpu, layout):
+    p = gen.int4_problem(515, 4096, 64, batch=2, seed=21, dist="ref")
+    check(run_int4(p, gpu, layout=layout, path=kq.PATH_MFMA, y_dtype=torch.float32),
+          ref_int4(p, layout), f"mfma {layout}")
+    rng = np.random.default_rng(5)
+    S = gen.bf16_bits(np.abs(rng.normal(0, 0.02, (515, 64))))
+    B = gen.bf16_bits(rng.normal(0, 0.02, (515, 64)))
+    ref = oracle.int4_gemv(p["W"], S, B, p["X"], 515, 4096, 64, 0, oracle.BF16)
+    check(run_int4(p, gpu, layout="split", sb_dtype=kq.BF16, S=S, B=B, path=kq.PATH_MFMA), ref,
+          "mfma bf16")
+
+
+@pytest.mark.parametrize("K,G", [(1024, 32), (2880, 64)])
+def test_mfma_unsupported_falls_back(gpu, K, G):
+    """The matrix-core path needs G in {64, 128} and K % 128 == 0; forcing it
+    otherwise is refused, and the automatic choice uses the vector path."""
+    p = gen.int4_problem(64, K, G, batch=8, seed=2)
+    with pytest.raises(kq.KQError) as e:
+        run_int4(p, gpu, path=kq.PATH_MFMA)
+    assert e.value.status == kq.KQ_EUNSUPPORTED
+    check(run_int4(p, gpu), ref_int4(p), f"auto path K={K} G={G}")
