@@ -181,10 +181,51 @@ def bench_roofline(torch, kq, dev, timer, res):
     b = int4_bytes(M, K)
     res["roofline"] = {"bound": "hbm", "achieved": round(b / us / 1e3, 1), "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-                       "traffic": None, "kernel": "int4_gemv_valu (4096x14336, batch 1)",
+                       "traffic": measured_traffic(), "kernel": "int4_gemv_valu (4096x14336, batch 1)",
                        "bytes_per_launch": b, "us_per_launch": round(us, 3),
                        "launches_timed": reps * N_LAYERS}
     del layers
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "int4_gemv_4096x14336_traffic.json")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs over the `traffic` section (each
+    counter scaled by what it reads for a torch copy kernel of known size).
+    Counters cannot be read live, so this is the recorded figure (or None)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)["traffic_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def bench_traffic(torch, kq, dev, res):
+    """Eager launches for the counter runs: the roofline kernel over its 32
+    weight copies, then a plain copy kernel (int32 -> fp32 elementwise copy,
+    COPY_BYTES read and COPY_BYTES written; a same-dtype copy_ would be a DMA
+    memcpy with no kernel) that calibrates FETCH_SIZE and WRITE_SIZE."""
+    M, K = 4096, 14336
+    layers = make_int4_layers(torch, dev, N_LAYERS, [("down", M, K)], seed=99)
+    x = torch.randn((1, K), device=dev).half()
+    y = torch.empty((1, M), dtype=torch.float16, device=dev)
+    for L in layers:
+        W, SB, _, _ = L["down"]
+        kq.int4_gemv(W, SB, x, y, kq.GemvParams(M, K, G))
+    torch.cuda.synchronize()
+    del layers
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    res["traffic_run"] = {"gemv_launches": N_LAYERS, "gemv_bytes": int4_bytes(M, K),
+                          "copy_launches": 4, "copy_bytes": COPY_BYTES}
+
+
+COPY_BYTES = 256 << 20
 
 
 # ---------------------------------------------------------------------------
@@ -385,6 +426,10 @@ def main():
         log("[bench] roofline kernel 4096x14336")
         bench_roofline(torch, kq, dev, timer, res)
         log(f"[bench] roofline {res['roofline']}")
+    if "traffic" in sections:
+        log("[bench] counter-run launches (roofline kernel + calibration copy)")
+        bench_traffic(torch, kq, dev, res)
+        log(f"[bench] traffic {res['traffic_run']}")
     if "moe" in sections:
         log("[bench] MoE block, 36 layers x 128 experts")
         bench_moe(torch, kq, dev, args, timer, res)

@@ -78,7 +78,7 @@ kq_status kq_int4_gemv(const uint32_t* W, const void* S, const void* B, kq_dtype
                        kq_stream_t stream);
 
 /* kq_int4_gemv with the kernel family forced (VALU dot2 path or MFMA
- * 32x32x16 path); used to measure the crossover. Same contract. */
+ * 16x16x32 path); used to measure the crossover. Same contract. */
 kq_status kq_int4_gemv_path(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,
                             const uint16_t* X, void* Y, kq_dtype y_dtype,
                             uint32_t M, uint32_t K, uint32_t G, uint32_t batch,
@@ -87,9 +87,10 @@ kq_status kq_int4_gemv_path(const uint32_t* W, const void* S, const void* B, kq_
 /* Tuning entry point: kq_int4_gemv with the kernel family and launch shape
  * forced. VALU: rows = rows per wave work item (1, 2, 4, 8), unroll = 64-chunk
  * steps per row held in registers (1, 2, 4, 8, 16; at least K/2048).
- * MFMA: rows = 32-row tiles per wave (1, 2), unroll = quant groups in flight
- * (1, 2, 4). Returns KQ_EUNSUPPORTED for a shape the family cannot run. Used
- * by the benchmark sweeps. */
+ * MFMA: rows = K parts P per workgroup (a divisor of K/128, at most 16),
+ * unroll = ring depth D in 128-k spans (2, 4, 8); 0 = automatic for either.
+ * Returns KQ_EUNSUPPORTED for a shape the family cannot run. Used by the
+ * benchmark sweeps and the tests. */
 kq_status kq_int4_gemv_cfg(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,
                            const uint16_t* X, void* Y, kq_dtype y_dtype,
                            uint32_t M, uint32_t K, uint32_t G, uint32_t batch,

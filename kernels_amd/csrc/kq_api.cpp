@@ -60,7 +60,11 @@ kq_status run_int4(const uint32_t* W, const void* S, const void* B, kq_dtype sb_
     kq::Int4Cfg mcfg = forced ? *forced : kq::int4_mfma_default(M, K, batch);
     const bool valu_ok = kq::int4_valu_supported(K, batch, vcfg);
     const bool mfma_ok = kq::int4_mfma_supported(K, G, batch, mcfg);
-    if (path == KQ_PATH_AUTO) path = (batch >= 8 && mfma_ok) || !valu_ok ? KQ_PATH_MFMA : KQ_PATH_VALU;
+    // measured crossover (bench.py skinny sweep): the vector path streams 1 KiB
+    // rows and wins at 1-2 tokens; from 3 tokens (two vector passes) the
+    // matrix cores win
+    if (path == KQ_PATH_AUTO)
+        path = (mfma_ok && batch >= 3) || !valu_ok ? KQ_PATH_MFMA : KQ_PATH_VALU;
     if (path == KQ_PATH_VALU) {
         if (!valu_ok) return KQ_EUNSUPPORTED;
         return hip_status(kq::launch_int4_valu(W, Sp, Bp, mk, inter, X, Y, yf, M, K, G, batch, vcfg, s));

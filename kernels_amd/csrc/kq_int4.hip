@@ -1,28 +1,33 @@
-// kq_int4.hip -- int4 group-affine GEMV, vector-ALU path (gfx950).
+// kq_int4.hip -- int4 group-affine GEMV, vector-ALU path (gfx950), plus the
+// xsum32 and streaming-read kernels.
 //
 // Math (reference: int4-gemv/src/kernels.metal:17-31,397-448):
 //   y[b,m] = sum_g S[m,g] * (sum_{k in g} q[m,k] x[b,k]) + B[m,g] * (sum_{k in g} x[b,k])
 // evaluated per 32-weight chunk so the bias term lands exactly once per chunk.
 //
-// Mapping on CDNA4 (a decode GEMV is one streaming read of W; everything here
-// serves keeping HBM requests in flight):
-//   * persistent grid: one 1024-thread workgroup (16 waves) per CU; a wave
-//     walks groups of R consecutive rows with a grid-wide stride, and each
-//     row group as segments of S 64-chunk steps ("items"), so x is staged
-//     once per CU and registers stay bounded for any K;
-//   * a wave issues the 16-byte loads of its first item BEFORE the workgroup
-//     stages x, and the next item's loads before computing the current one
-//     (register double buffering), so the first HBM round trip overlaps the
-//     staging and later ones overlap the math;
-//   * x is staged in LDS as permuted fp16 pairs ([token][word%4][chunk], 16 B
-//     per word: lane-consecutive chunks are conflict-free ds_read_b128) plus
-//     per-chunk (sum, offset constant) -- this replaces the reference's
-//     separate xsum32 launch; all staging loads of a thread are issued first;
-//   * lane l owns chunk l + 64 s (s < S) of each row: a wave instruction reads
-//     1 KiB of a row; nibbles become fp16 by AND-OR into fp16 exponents
-//     (kq_device.h) and meet x in v_dot2_f32_f16 (fp32 accumulation); the
-//     group metadata is applied once per chunk: acc += s*(d - xc) + b*xs;
-//   * rows reduce with a wave64 butterfly; lane 0 stores y.
+// Mapping on CDNA4 (a decode GEMV is one streaming read of W):
+//   * a wave instruction reads 1 KiB of one row (lane l loads 16-byte chunk
+//     64*step + l): whole 128-byte lines per row, the access shape that runs
+//     at the streaming-read rate (shapes with 64-byte row pieces lose ~20%);
+//   * nibbles become fp16 by AND-OR into fp16 exponents (kq_device.h) and meet
+//     x in v_dot2_f32_f16 (fp32 accumulation): 1 shift + 4 AND-OR + 4 dot2
+//     per 8 weights and token-independent dequant; the group metadata is
+//     applied once per chunk: acc += s*(d - xc) + b*xs;
+//   * x is staged once per workgroup in LDS as permuted fp16 pairs
+//     [token][word%4][chunk] (lane-consecutive chunks: conflict-free
+//     ds_read_b128) plus per-chunk (sum, offset constant), with the chunks
+//     padded to a multiple of 64 by zeros: a lane past the end of a row
+//     contributes exactly 0 and no lane tests bounds;
+//   * a workgroup of P*Q waves owns a contiguous range of row groups (R rows
+//     each); wave (p, q) takes K-part p (J = steps/P consecutive steps) of row
+//     groups q, q+Q, ... ("rounds"). With P = 1 a wave finishes its rows alone
+//     (wave64 DPP reduction, store); with P > 1 (short matrices, to fill the
+//     CUs) the P partial sums of a round meet in LDS in a fixed order;
+//   * each wave streams its (row group, step) items through a ring of D
+//     register slots; every load is unconditional (rows and padding steps are
+//     clamped to valid addresses, results discarded) and first used by the
+//     compute of its own item, and the prologue's issue order is pinned, so
+//     the waitcnt pass waits for exactly one slot at a time.
 #include "kq_device.h"
 #include "kq_internal.h"
 
@@ -30,203 +35,254 @@ namespace kq {
 
 namespace {
 
-constexpr int kMaxThreads = 1024;
-constexpr int kStageRound = 2;  // x words per thread per staging round
+constexpr int kMaxWaves = 16;
+
+struct VArgs {
+    const uint32_t* W;
+    const uint16_t* S;  // interleaved (scale, bias) pairs, or scales
+    const uint16_t* B;  // biases (separate layout only)
+    const uint16_t* X;  // [ntok][K]
+    void* Y;            // [ntok][M]
+    uint32_t M, K, ntok, y_f32;
+    uint32_t nch, nchp, gpr, cshift;  // chunks per row (padded to 64), groups per row, log2(G/32)
+    uint32_t P, Q, J;                 // K parts, row-group lanes, steps per part
+    uint32_t groups_wg, ngroups;      // row groups per workgroup / in total
+    uint32_t rounds, nreal, nsteps;   // rounds per workgroup; items per wave, padded to D
+};
+
+struct VPlan {
+    uint32_t R, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D;
+    size_t lds;
+};
+
+template <int R>
+struct VSlot {
+    u32x4 w[R];
+    uint32_t s[R], b[R];  // interleaved: s holds (scale | bias << 16); else separate halves
+};
+
+// The four fp16-pair operands of one packed word (see kq_device.h).
+__device__ __forceinline__ u32x4 dq4(uint32_t w, const DequantConsts& k) {
+    const uint32_t w8 = w >> 8;
+    return u32x4{and_or(w, k.lo, k.e1024), and_or(w, k.hi, k.e64), and_or(w8, k.lo, k.e1024),
+                 and_or(w8, k.hi, k.e64)};
+}
+
+__device__ __forceinline__ float dot4(u32x4 d, u32x4 p, float acc) {
+    acc = dot2(d.x, p.x, acc);
+    acc = dot2(d.y, p.y, acc);
+    acc = dot2(d.z, p.z, acc);
+    return dot2(d.w, p.w, acc);
+}
 
 template <bool BF>
-__device__ __forceinline__ float meta_f(uint32_t v) {
+__device__ __forceinline__ float mval(uint32_t v) {
     if constexpr (BF) return bf2f((uint16_t)v);
     else return h2f((uint16_t)v);
 }
 
-// Staging of NB activation vectors into LDS, in two phases so the x loads
-// can be issued before the weight loads: the memory counter (vmcnt) retires
-// in order, so x must be ahead of W in the queue or staging would wait for
-// the first weight round trip.
-template <int NB>
-__device__ __forceinline__ void stage_x_load(const uint16_t* __restrict__ X, uint32_t K,
-                                             uint32_t w0, u32x4 (&v)[kStageRound]) {
-    const uint32_t nw = K >> 3, total = NB * nw, nthr = blockDim.x;
-#pragma unroll
-    for (int q = 0; q < kStageRound; ++q) {
-        const uint32_t w = w0 + q * nthr + threadIdx.x;
-        v[q] = u32x4{0, 0, 0, 0};
-        if (w < total) {
-            const uint32_t t = w / nw, wi = w - t * nw;
-            v[q] = *reinterpret_cast<const u32x4*>(X + (size_t)t * K + (size_t)wi * 8);
+struct Cursor {
+    uint32_t j, round;
+    __device__ __forceinline__ void advance(uint32_t J) {
+        if (++j == J) {
+            j = 0;
+            ++round;
         }
     }
+};
+
+__host__ __device__ inline size_t vlds_x(uint32_t ntok, uint32_t nchp) {
+    return (size_t)ntok * nchp * 72;
 }
 
-template <int NB>
-__device__ __forceinline__ void stage_x_store(uint32_t K, uint32_t w0,
-                                              const u32x4 (&v)[kStageRound], u32x4* xp,
-                                              float2* xk) {
-    const uint32_t nch = K >> 5, nw = K >> 3, total = NB * nw, nthr = blockDim.x;
-#pragma unroll
-    for (int q = 0; q < kStageRound; ++q) {
-        const uint32_t w = w0 + q * nthr + threadIdx.x;
-        float s, c;
-        word_consts(v[q], s, c);
-        s = quad_sum(s);
-        c = quad_sum(c);
-        if (w < total) {
-            const uint32_t t = w / nw, wi = w - t * nw;
-            const uint32_t ch = wi >> 2, j = wi & 3;
-            xp[(t * 4 + j) * nch + ch] = pair_perm(v[q]);
-            if (j == 0) xk[t * nch + ch] = make_float2(s, c);
-        }
-    }
-}
-
-// Issue the loads of one item: rows rg*R .. rg*R+R-1, steps seg*S .. seg*S+S-1.
-// SB: interleaved (scale, bias) dword per group; else separate S and B.
-template <int S, int R, bool SB>
-__device__ __forceinline__ void load_item(const uint32_t* __restrict__ W,
-                                          const uint16_t* __restrict__ Sm,
-                                          const uint16_t* __restrict__ Bm, uint32_t rg,
-                                          uint32_t seg, uint32_t M, uint32_t nch, uint32_t gpr,
-                                          uint32_t cshift, int lane, u32x4 (&w)[R][S],
-                                          uint32_t (&m)[R][S]) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t row = min(rg * R + r, M - 1);
-        const u32x4* wrow = reinterpret_cast<const u32x4*>(W) + (size_t)row * nch;
-        const uint32_t mrow = row * gpr;
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const uint32_t c0 = 64u * (seg * S + s);
-            if (c0 < nch) {  // wave-uniform
-                const uint32_t c = c0 + 64 <= nch ? c0 + lane : min(c0 + lane, nch - 1);
-                w[r][s] = ldg_nt(wrow + c);
-                const uint32_t mi = mrow + (c >> cshift);
-                if constexpr (SB)
-                    m[r][s] = reinterpret_cast<const uint32_t*>(Sm)[mi];
-                else
-                    m[r][s] = (uint32_t)Sm[mi] | ((uint32_t)Bm[mi] << 16);
-            }
-        }
-    }
-}
-
-template <int NB, int S, int R, bool BF>
-__device__ __forceinline__ void compute_item(const u32x4 (&w)[R][S], const uint32_t (&m)[R][S],
-                                             const u32x4* xp, const float2* xk, uint32_t nch,
-                                             int lane, uint32_t seg, const DequantConsts& kc,
-                                             float (&acc)[R][NB]) {
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-        const uint32_t c0 = 64u * (seg * S + s), c = c0 + lane;
-        if (c0 < nch && c < nch) {
-#pragma unroll
-            for (int t = 0; t < NB; ++t) {
-                const u32x4 p0 = xp[(t * 4 + 0) * nch + c];
-                const u32x4 p1 = xp[(t * 4 + 1) * nch + c];
-                const u32x4 p2 = xp[(t * 4 + 2) * nch + c];
-                const u32x4 p3 = xp[(t * 4 + 3) * nch + c];
-                const float2 k2 = xk[t * nch + c];
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const u32x4 q = w[r][s];
-                    float da = qdot8(q.x, p0, 0.0f, kc);
-                    float db = qdot8(q.y, p1, 0.0f, kc);
-                    da = qdot8(q.z, p2, da, kc);
-                    db = qdot8(q.w, p3, db, kc);
-                    const float sc = meta_f<BF>(m[r][s] & 0xFFFFu);
-                    const float bi = meta_f<BF>(m[r][s] >> 16);
-                    acc[r][t] = fmaf(sc, (da + db) - k2.y, fmaf(bi, k2.x, acc[r][t]));
-                }
-            }
-        }
-    }
-}
-
-// Wave-reduce a row group's accumulators, store y, reset the accumulators.
-template <int NB, int R>
-__device__ __forceinline__ void store_rows(float (&acc)[R][NB], int lane, uint32_t rg, uint32_t M,
-                                           void* __restrict__ Y, int y_f32) {
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int t = 0; t < NB; ++t) {
-            const float v = wave_sum(acc[r][t]);
-            acc[r][t] = 0.0f;
-            const uint32_t row = rg * R + r;
-            if (lane == 0 && row < M) {
-                const size_t o = (size_t)t * M + row;
-                if (y_f32) reinterpret_cast<float*>(Y)[o] = v;
-                else reinterpret_cast<uint16_t*>(Y)[o] = f2h(v);
-            }
-        }
-}
-
-// NB tokens; R rows per group; S 64-chunk steps per item (a row group is
-// nseg = ceil(K/32/64/S) items). Items are double-buffered in registers.
-template <int NB, int S, int R, bool SB, bool BF>
-__global__ __launch_bounds__(kMaxThreads) void int4_gemv_valu(
-    const uint32_t* __restrict__ W, const uint16_t* __restrict__ Sm,
-    const uint16_t* __restrict__ Bm, const uint16_t* __restrict__ X, void* __restrict__ Y,
-    int y_f32, uint32_t M, uint32_t K, uint32_t gshift) {
+template <int NB, int R, int D, bool SB, bool BF>
+__global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const uint32_t nch = K >> 5;
-    u32x4* xp = reinterpret_cast<u32x4*>(smem);                           // [NB][4][nch]
-    float2* xk = reinterpret_cast<float2*>(smem + (size_t)NB * nch * 64);  // [NB][nch]
-    const int lane = threadIdx.x & 63;
-    const uint32_t nwaves = blockDim.x >> 6;
-    const uint32_t stride = gridDim.x * nwaves;
-    const uint32_t groups = (M + R - 1) / R;
-    const uint32_t nseg = (((nch + 63) >> 6) + S - 1) / S;
-    const uint32_t gpr = K >> gshift, cshift = gshift - 5;
-    const uint32_t xwords = NB * (K >> 3), xround = blockDim.x * kStageRound;
-    const DequantConsts kc;
+    const uint32_t nch = A.nch, nchp = A.nchp, nw = A.K >> 3;
+    u32x4* xp = reinterpret_cast<u32x4*>(smem);                             // [NB][4][nchp]
+    float2* xk = reinterpret_cast<float2*>(smem + (size_t)NB * nchp * 64);  // [NB][nchp]
+    float* part = reinterpret_cast<float*>(smem + vlds_x(NB, nchp));        // [2][waves][R*NB]
 
-    u32x4 wa[R][S], wb[R][S];
-    uint32_t ma[R][S], mb[R][S];
+    const uint32_t tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & 63;
+    const uint32_t wave = tid >> 6, p = wave % A.P, q = wave / A.P;
+    const uint32_t g0 = blockIdx.x * A.groups_wg;
+    const uint32_t last_group = A.ngroups - 1, last_row = A.M - 1;
+    const u32x4* W4 = reinterpret_cast<const u32x4*>(A.W);
+
+    // ---- 1. x staging loads first (vmcnt retires in order)
+    const uint32_t xtotal = NB * nw;
+    const u32x4* X4 = reinterpret_cast<const u32x4*>(A.X);
+    constexpr int kXr = 2;
+    u32x4 sv[kXr];
+    auto x_load = [&](uint32_t w0) {
+#pragma unroll
+        for (int r = 0; r < kXr; ++r) {
+            const uint32_t w = w0 + r * nthr + tid;
+            sv[r] = X4[w < xtotal ? w : xtotal - 1];
+        }
+    };
+    auto x_store = [&](uint32_t w0) {
+#pragma unroll
+        for (int r = 0; r < kXr; ++r) {
+            const uint32_t w = w0 + r * nthr + tid;
+            float s, c;
+            word_consts(sv[r], s, c);
+            s = quad_sum(s);
+            c = quad_sum(c);
+            if (w < xtotal) {
+                const uint32_t t = w / nw, wi = w - t * nw, ch = wi >> 2, j = wi & 3;
+                xp[(t * 4 + j) * nchp + ch] = pair_perm(sv[r]);
+                if (j == 0) xk[t * nchp + ch] = make_float2(s, c);
+            }
+        }
+    };
+    x_load(0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 2. prime the ring
+    VSlot<R> ring[D];
+    auto issue = [&](VSlot<R>& e, Cursor c) {
+        if (c.round >= A.rounds) {  // padding item: re-read the last real one
+            c.round = A.rounds - 1;
+            c.j = A.J - 1;
+        }
+        const uint32_t grp = min(g0 + c.round * A.Q + q, last_group);
+        const uint32_t ch = min((p * A.J + c.j) * 64 + lane, nch - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = min(grp * R + r, last_row);
+            e.w[r] = ldg_nt(W4 + (size_t)row * nch + ch);
+            const size_t gi = (size_t)row * A.gpr + (ch >> A.cshift);
+            if constexpr (SB) {
+                e.s[r] = reinterpret_cast<const uint32_t*>(A.S)[gi];
+            } else {
+                e.s[r] = A.S[gi];
+                e.b[r] = A.B[gi];
+            }
+        }
+    };
+    Cursor ci{0, 0};
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        issue(ring[d], ci);
+        ci.advance(A.J);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- 3. finish the staging, zero the padding chunks
+    x_store(0);
+    for (uint32_t w0 = kXr * nthr; w0 < xtotal; w0 += kXr * nthr) {
+        x_load(w0);
+        x_store(w0);
+    }
+    const uint32_t npad = nchp - nch;
+    for (uint32_t i = tid; i < NB * 5 * npad; i += nthr) {
+        const uint32_t t = i / (5 * npad), rem = i - t * 5 * npad, j = rem / npad;
+        const uint32_t ch = nch + (rem - j * npad);
+        if (j < 4) xp[(t * 4 + j) * nchp + ch] = u32x4{0, 0, 0, 0};
+        else xk[t * nchp + ch] = make_float2(0.0f, 0.0f);
+    }
+    __syncthreads();
+
+    const DequantConsts kc;
     float acc[R][NB];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int t = 0; t < NB; ++t) acc[r][t] = 0.0f;
 
-    // first staging round's x loads, then this wave's first item, then the
-    // rest of the staging
-    uint32_t rg = blockIdx.x * nwaves + (threadIdx.x >> 6), seg = 0;
-    u32x4 xv[kStageRound];
-    stage_x_load<NB>(X, K, 0, xv);
-    if (rg < groups) load_item<S, R, SB>(W, Sm, Bm, rg, 0, M, nch, gpr, cshift, lane, wa, ma);
-    stage_x_store<NB>(K, 0, xv, xp, xk);
-    for (uint32_t w0 = xround; w0 < xwords; w0 += xround) {
-        stage_x_load<NB>(X, K, w0, xv);
-        stage_x_store<NB>(K, w0, xv, xp, xk);
-    }
-    __syncthreads();
-
-    auto advance = [&](uint32_t& g, uint32_t& sg) {
-        if (++sg == nseg) { sg = 0; g += stride; }
+    auto store = [&](uint32_t row, int t, float v) {
+        const size_t o = (size_t)t * A.M + row;
+        if (A.y_f32) reinterpret_cast<float*>(A.Y)[o] = v;
+        else reinterpret_cast<uint16_t*>(A.Y)[o] = f2h(v);
     };
-    while (rg < groups) {
-        uint32_t nrg = rg, nsg = seg;
-        advance(nrg, nsg);
-        if (nrg < groups)
-            load_item<S, R, SB>(W, Sm, Bm, nrg, nsg, M, nch, gpr, cshift, lane, wb, mb);
-        compute_item<NB, S, R, BF>(wa, ma, xp, xk, nch, lane, seg, kc, acc);
-        if (seg == nseg - 1) store_rows<NB, R>(acc, lane, rg, M, Y, y_f32);
-        rg = nrg;
-        seg = nsg;
-        if (rg >= groups) break;
-        advance(nrg, nsg);
-        if (nrg < groups)
-            load_item<S, R, SB>(W, Sm, Bm, nrg, nsg, M, nch, gpr, cshift, lane, wa, ma);
-        compute_item<NB, S, R, BF>(wb, mb, xp, xk, nch, lane, seg, kc, acc);
-        if (seg == nseg - 1) store_rows<NB, R>(acc, lane, rg, M, Y, y_f32);
-        rg = nrg;
-        seg = nsg;
+    auto finish = [&](uint32_t round) {
+        const uint32_t gl = round * A.Q + q, grp = g0 + gl;
+        if (A.P == 1) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int t = 0; t < NB; ++t) {
+                    const float v = wave_sum(acc[r][t]);
+                    acc[r][t] = 0.0f;
+                    const uint32_t row = grp * R + r;
+                    if (lane == 0 && gl < A.groups_wg && grp < A.ngroups && row < A.M)
+                        store(row, t, v);
+                }
+            return;
+        }
+        float* pw = part + ((size_t)(round & 1) * (A.P * A.Q) + wave) * (R * NB);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                const float v = wave_sum(acc[r][t]);
+                acc[r][t] = 0.0f;
+                if (lane == 0) pw[r * NB + t] = v;
+            }
+        __syncthreads();
+        const float* pr = part + (size_t)(round & 1) * (A.P * A.Q) * (R * NB);
+        const uint32_t nout = A.Q * R * NB;
+        for (uint32_t i = tid; i < nout; i += nthr) {
+            const uint32_t qq = i / (R * NB), rt = i - qq * (R * NB);
+            float v = 0.0f;
+            for (uint32_t pp = 0; pp < A.P; ++pp) v += pr[(qq * A.P + pp) * (R * NB) + rt];
+            const uint32_t gq = round * A.Q + qq, gg = g0 + gq, row = gg * R + rt / NB;
+            if (gq < A.groups_wg && gg < A.ngroups && row < A.M) store(row, rt % NB, v);
+        }
+    };
+    auto step = [&](const VSlot<R>& e, Cursor c, uint32_t n) {
+        const uint32_t ch = (p * A.J + c.j) * 64 + lane;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const u32x4 d0 = dq4(e.w[r].x, kc), d1 = dq4(e.w[r].y, kc);
+            const u32x4 d2 = dq4(e.w[r].z, kc), d3 = dq4(e.w[r].w, kc);
+            float sc, bi;
+            if constexpr (SB) {
+                sc = mval<BF>(e.s[r] & 0xFFFFu);
+                bi = mval<BF>(e.s[r] >> 16);
+            } else {
+                sc = mval<BF>(e.s[r]);
+                bi = mval<BF>(e.b[r]);
+            }
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                const u32x4 p0 = xp[(t * 4 + 0) * nchp + ch];
+                const u32x4 p1 = xp[(t * 4 + 1) * nchp + ch];
+                const u32x4 p2 = xp[(t * 4 + 2) * nchp + ch];
+                const u32x4 p3 = xp[(t * 4 + 3) * nchp + ch];
+                const float2 k2 = xk[t * nchp + ch];
+                const float da = dot4(d2, p2, dot4(d0, p0, 0.0f));
+                const float db = dot4(d3, p3, dot4(d1, p1, 0.0f));
+                acc[r][t] = fmaf(sc, (da + db) - k2.y, fmaf(bi, k2.x, acc[r][t]));
+            }
+        }
+        if (n < A.nreal && c.j == A.J - 1) finish(c.round);
+    };
+
+    // ---- 4. main loop (loads D items ahead), then the last D items
+    Cursor cc{0, 0};
+    uint32_t n = 0;
+    for (; n + D < A.nsteps; n += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            step(ring[d], cc, n + d);
+            cc.advance(A.J);
+            issue(ring[d], ci);
+            ci.advance(A.J);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        step(ring[d], cc, n + d);
+        cc.advance(A.J);
     }
 }
 
 int g_num_cu = 0;
 
-int num_cu() {
+uint32_t num_cu() {
     if (g_num_cu <= 0) {
         int dev = 0, n = 0;
         if (hipGetDevice(&dev) == hipSuccess &&
@@ -236,48 +292,11 @@ int num_cu() {
         else
             g_num_cu = 256;
     }
-    return g_num_cu;
+    return (uint32_t)g_num_cu;
 }
 
-template <int NB, int S, int R>
-hipError_t launch3(const uint32_t* W, const uint16_t* Sm, const uint16_t* Bm, int bf16, bool sb,
-                   const uint16_t* X, void* Y, bool y_f32, uint32_t M, uint32_t K,
-                   uint32_t gshift, hipStream_t s) {
-    const uint32_t groups = (M + R - 1) / R;
-    const uint32_t waves = 16;
-    uint32_t blocks = (groups + waves - 1) / waves;
-    const uint32_t ncu = (uint32_t)num_cu();
-    if (blocks > ncu) blocks = ncu;
-    const size_t lds = (size_t)NB * (K >> 5) * 72;
-    const int yf = y_f32 ? 1 : 0;
-#define KQ_GO(SBV, BFV)                                                                        \
-    int4_gemv_valu<NB, S, R, SBV, BFV><<<blocks, waves * 64, lds, s>>>(W, Sm, Bm, X, Y, yf, M, \
-                                                                       K, gshift)
-    if (sb && !bf16) KQ_GO(true, false);
-    else if (!sb && !bf16) KQ_GO(false, false);
-    else if (sb) KQ_GO(true, true);
-    else KQ_GO(false, true);
-#undef KQ_GO
-    return hipGetLastError();
-}
-
-template <int NB>
-hipError_t launch_nb(Int4Cfg cfg, const uint32_t* W, const uint16_t* Sm, const uint16_t* Bm,
-                     int bf16, bool sb, const uint16_t* X, void* Y, bool y_f32, uint32_t M,
-                     uint32_t K, uint32_t gshift, hipStream_t s) {
-#define KQ_CASE(SS, RR)                                                                   \
-    if (cfg.unroll == SS && cfg.rows == RR)                                               \
-        return launch3<NB, SS, RR>(W, Sm, Bm, bf16, sb, X, Y, y_f32, M, K, gshift, s);
-    if constexpr (NB == 1) {
-        KQ_CASE(1, 1) KQ_CASE(1, 2) KQ_CASE(1, 4) KQ_CASE(2, 1) KQ_CASE(2, 2) KQ_CASE(4, 1)
-    } else if constexpr (NB == 2) {
-        KQ_CASE(1, 1) KQ_CASE(1, 2) KQ_CASE(2, 1) KQ_CASE(2, 2) KQ_CASE(4, 1)
-    } else {
-        KQ_CASE(1, 1) KQ_CASE(2, 1) KQ_CASE(4, 1)
-    }
-#undef KQ_CASE
-    return hipErrorInvalidValue;
-}
+constexpr size_t kLdsMax = 160 * 1024;
+constexpr uint32_t kMaxNB = 2;  // tokens per pass of the vector path
 
 uint32_t log2u(uint32_t v) {
     uint32_t r = 0;
@@ -285,49 +304,139 @@ uint32_t log2u(uint32_t v) {
     return r;
 }
 
-uint32_t steps_for(uint32_t K) { return ((K >> 5) + 63) / 64; }
+// Launch plan: R rows per item, P K-parts, Q row-group lanes, ring depth D.
+// Measured on MI355X (Llama / 70B shapes, batch 1): once running the kernel
+// streams at ~5.9 TB/s and a launch costs ~3.2 us on top, so the plan (1)
+// spreads the row groups over every CU, (2) keeps the per-CU bytes minimal
+// (no idle lanes: Q is cut to the rows a CU has), and (3) uses D = 2 -- deeper
+// rings measured slower at every shape (more rows open at once per CU).
+// Among (R, P) with equal per-CU work, one x read shared by 2 rows and fewer
+// K parts (no LDS reduction) win.
+bool make_vplan(uint32_t M, uint32_t K, uint32_t ntok, Int4Cfg cfg, VPlan& out) {
+    const uint32_t nch = K >> 5, nstep = (nch + 63) / 64, nchp = nstep * 64, cu = num_cu();
+    if (cfg.unroll != 0 && cfg.unroll != 2 && cfg.unroll != 4 && cfg.unroll != 8) return false;
+    bool found = false;
+    double best = 0.0;
+    for (uint32_t R = 2; R >= 1; --R) {
+        for (uint32_t P = 1; P <= kMaxWaves; ++P) {
+            if (nstep % P) continue;
+            if (cfg.rows > 0 && (uint32_t)cfg.rows != P) continue;
+            const uint32_t D = cfg.unroll > 0 ? (uint32_t)cfg.unroll : 2;
+            if (R == 2 && D == 8) continue;  // register budget: 2 rows x 8 slots
+            const uint32_t ngroups = (M + R - 1) / R, J = nstep / P;
+            const uint32_t per_cu = (ngroups + cu - 1) / cu;
+            const uint32_t qmax = kMaxWaves / P;
+            const uint32_t rounds = (per_cu + qmax - 1) / qmax;
+            const uint32_t Q = (per_cu + rounds - 1) / rounds;
+            const uint32_t waves = P * Q, groups_wg = rounds * Q;
+            const uint32_t nwg = (ngroups + groups_wg - 1) / groups_wg;
+            const uint32_t nreal = rounds * J;
+            const uint32_t nsteps = (nreal + D - 1) / D * D;
+            const size_t lds = vlds_x(ntok, nchp) + (P > 1 ? (size_t)2 * waves * R * ntok * 4 : 0);
+            if (lds > kLdsMax) continue;
+            // per-CU KiB (padding included) plus a latency term for short
+            // waves: fewer than 8 waves or fewer than 2 items leave HBM idle
+            double cost = (double)nsteps * waves * R;
+            if (waves < 8) cost *= 1.0 + 0.1 * (8 - waves);
+            if (P > 1) cost *= 1.02;
+            if (R == 2) cost *= 0.98;
+            if (!found || cost < best) {
+                found = true;
+                best = cost;
+                out = VPlan{R, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, lds};
+            }
+        }
+    }
+    return found;
+}
+
+template <int NB, int R, int D, bool SB, bool BF>
+hipError_t vgo(const VArgs& a, const VPlan& pl, hipStream_t s) {
+    auto kern = int4_valu<NB, R, D, SB, BF>;
+    if (pl.lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)pl.lds);
+        if (e != hipSuccess) return e;
+    }
+    kern<<<pl.nwg, pl.P * pl.Q * 64, pl.lds, s>>>(a);
+    return hipGetLastError();
+}
+
+template <int NB, int R, bool SB, bool BF>
+hipError_t vgo_d(const VArgs& a, const VPlan& pl, hipStream_t s) {
+    switch (pl.D) {
+        case 2: return vgo<NB, R, 2, SB, BF>(a, pl, s);
+        case 4: return vgo<NB, R, 4, SB, BF>(a, pl, s);
+        case 8:
+            if constexpr (R == 1) return vgo<NB, R, 8, SB, BF>(a, pl, s);
+            else return hipErrorInvalidValue;
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int NB, bool SB, bool BF>
+hipError_t vgo_r(const VArgs& a, const VPlan& pl, hipStream_t s) {
+    return pl.R == 2 ? vgo_d<NB, 2, SB, BF>(a, pl, s) : vgo_d<NB, 1, SB, BF>(a, pl, s);
+}
+
+template <int NB>
+hipError_t vgo_nb(const VArgs& a, const VPlan& pl, bool sb, bool bf, hipStream_t s) {
+    if (sb) return bf ? vgo_r<NB, true, true>(a, pl, s) : vgo_r<NB, true, false>(a, pl, s);
+    return bf ? vgo_r<NB, false, true>(a, pl, s) : vgo_r<NB, false, false>(a, pl, s);
+}
 
 }  // namespace
 
-size_t int4_valu_lds_bytes(uint32_t K, uint32_t batch) { return (size_t)batch * (K >> 5) * 72; }
+Int4Cfg int4_valu_default(uint32_t, uint32_t, uint32_t) { return Int4Cfg{0, 0}; }
+
+size_t int4_valu_lds_bytes(uint32_t K, uint32_t batch) {
+    const uint32_t nchp = ((K >> 5) + 63) / 64 * 64;
+    return vlds_x(batch < kMaxNB ? batch : kMaxNB, nchp);
+}
 
 bool int4_valu_supported(uint32_t K, uint32_t batch, Int4Cfg cfg) {
     if (batch < 1 || batch > 16) return false;
-    const int S = cfg.unroll, R = cfg.rows;
-    const bool ok = (S == 1 && (R == 1 || R == 2 || R == 4)) || (S == 2 && (R == 1 || R == 2)) ||
-                    (S == 4 && R == 1);
-    return ok && int4_valu_lds_bytes(K, 1) <= 65536;
-}
-
-Int4Cfg int4_valu_default(uint32_t M, uint32_t K, uint32_t batch) {
-    (void)M;
-    const uint32_t st = steps_for(K);
-    Int4Cfg c;
-    c.unroll = st <= 1 ? 1 : st <= 2 ? 2 : 4;
-    c.rows = c.unroll == 1 ? 4 : c.unroll == 2 ? 2 : 1;
-    // more tokens per pass keep more x pairs live: hold rows*tokens <= 4
-    const int nb = batch >= 4 ? 4 : batch >= 2 ? 2 : 1;
-    while (c.rows > 1 && c.rows * nb > 4) c.rows /= 2;
-    return c;
+    VPlan pl;
+    return make_vplan(16, K, 1, cfg, pl);
 }
 
 hipError_t launch_int4_valu(const uint32_t* W, const uint16_t* S, const uint16_t* B, int meta_kind,
                             bool interleaved, const uint16_t* X, void* Y, bool y_f32, uint32_t M,
                             uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg, hipStream_t s) {
-    const uint32_t gshift = log2u(G);
     const size_t ysz = y_f32 ? 4 : 2;
-    // tokens in groups of 4, 2, 1 (each group one pass over W)
     for (uint32_t t0 = 0; t0 < batch;) {
-        const uint32_t left = batch - t0;
-        uint32_t nb = (left >= 4 && int4_valu_lds_bytes(K, 4) <= 65536) ? 4
-                    : (left >= 2 && int4_valu_lds_bytes(K, 2) <= 65536) ? 2 : 1;
-        while (nb > 1 && cfg.rows * (int)nb > 4) nb /= 2;  // register budget
-        const uint16_t* Xt = X + (size_t)t0 * K;
-        void* Yt = reinterpret_cast<uint8_t*>(Y) + (size_t)t0 * M * ysz;
-        hipError_t e;
-        if (nb == 4) e = launch_nb<4>(cfg, W, S, B, meta_kind, interleaved, Xt, Yt, y_f32, M, K, gshift, s);
-        else if (nb == 2) e = launch_nb<2>(cfg, W, S, B, meta_kind, interleaved, Xt, Yt, y_f32, M, K, gshift, s);
-        else e = launch_nb<1>(cfg, W, S, B, meta_kind, interleaved, Xt, Yt, y_f32, M, K, gshift, s);
+        uint32_t nb = batch - t0 >= kMaxNB ? kMaxNB : 1;
+        VPlan pl;
+        if (!make_vplan(M, K, nb, cfg, pl)) {
+            if (nb == 1 || !make_vplan(M, K, 1, cfg, pl)) return hipErrorInvalidValue;
+            nb = 1;
+        }
+        VArgs a;
+        a.W = W;
+        a.S = S;
+        a.B = B;
+        a.X = X + (size_t)t0 * K;
+        a.Y = reinterpret_cast<uint8_t*>(Y) + (size_t)t0 * M * ysz;
+        a.M = M;
+        a.K = K;
+        a.ntok = nb;
+        a.y_f32 = y_f32 ? 1 : 0;
+        a.nch = K >> 5;
+        a.nchp = ((K >> 5) + 63) / 64 * 64;
+        a.gpr = K / G;
+        a.cshift = log2u(G) - 5;
+        a.P = pl.P;
+        a.Q = pl.Q;
+        a.J = pl.J;
+        a.groups_wg = pl.groups_wg;
+        a.ngroups = (M + pl.R - 1) / pl.R;
+        a.rounds = pl.rounds;
+        a.nreal = pl.nreal;
+        a.nsteps = pl.nsteps;
+        const bool bf = meta_kind == 1;
+        const hipError_t e = nb == 2 ? vgo_nb<2>(a, pl, interleaved, bf, s)
+                                     : vgo_nb<1>(a, pl, interleaved, bf, s);
         if (e != hipSuccess) return e;
         t0 += nb;
     }

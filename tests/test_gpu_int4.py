@@ -52,38 +52,49 @@ def test_config0_4096x4096(gpu):
     print(f"config0 inf-rel err {inf_rel(got, ref):.2e}")
 
 
+PATHS = [kq.PATH_VALU, kq.PATH_MFMA]
+
+
+@pytest.mark.parametrize("path", PATHS)
 @pytest.mark.parametrize("M,K", [(1024, 4096), (14336, 4096), (4096, 14336)])
-def test_llama_layer_shapes(gpu, M, K):
+def test_llama_layer_shapes(gpu, M, K, path):
     p = gen.int4_problem(M, K, 64, seed=M + K)
-    check(run_int4(p, gpu), ref_int4(p), f"{M}x{K}")
+    check(run_int4(p, gpu, path=path), ref_int4(p), f"{M}x{K} path {path}")
 
 
+@pytest.mark.parametrize("path", PATHS)
 @pytest.mark.parametrize("layout", ["sb", "split"])
 @pytest.mark.parametrize("ydt", [torch.float16, torch.float32])
-def test_layouts_and_output_dtype(gpu, layout, ydt):
+def test_layouts_and_output_dtype(gpu, layout, ydt, path):
     p = gen.int4_problem(1000, 2048, 64, seed=7, dist="ref")
-    check(run_int4(p, gpu, layout=layout, y_dtype=ydt), ref_int4(p, layout), f"{layout} {ydt}")
+    check(run_int4(p, gpu, layout=layout, y_dtype=ydt, path=path), ref_int4(p, layout),
+          f"{layout} {ydt} path {path}")
 
 
-def test_bf16_metadata(gpu):
+@pytest.mark.parametrize("path", PATHS)
+def test_bf16_metadata(gpu, path):
     p = gen.int4_problem(512, 1024, 64, seed=3)
     rng = np.random.default_rng(0)
     S = gen.bf16_bits(np.abs(rng.normal(0, 0.02, (512, 16))))
     B = gen.bf16_bits(rng.normal(0, 0.02, (512, 16)))
     SB = np.ascontiguousarray(np.stack([S, B], -1))
     ref = oracle.int4_gemv(p["W"], S, B, p["X"], 512, 1024, 64, 0, oracle.BF16)
-    check(run_int4(p, gpu, layout="split", sb_dtype=kq.BF16, S=S, B=B), ref, "bf16 split")
-    check(run_int4(p, gpu, layout="sb", sb_dtype=kq.BF16, S=SB), ref, "bf16 sb")
+    check(run_int4(p, gpu, layout="split", sb_dtype=kq.BF16, S=S, B=B, path=path), ref,
+          "bf16 split")
+    check(run_int4(p, gpu, layout="sb", sb_dtype=kq.BF16, S=SB, path=path), ref, "bf16 sb")
 
 
+@pytest.mark.parametrize("path", PATHS)
 @pytest.mark.parametrize("G", [32, 64, 128])
 @pytest.mark.parametrize("M,K", [(1, 512), (7, 4096), (4097, 1024), (300, 2880), (65, 32 * 64),
-                                 (33, 28672)])
-def test_edge_shapes_and_groups(gpu, M, K, G):
+                                 (33, 28672), (2, 32)])
+def test_edge_shapes_and_groups(gpu, M, K, G, path):
     if K % G:
         pytest.skip("K % G")
+    if path == kq.PATH_MFMA and K % 128:
+        pytest.skip("matrix-core path needs K % 128 == 0")
     p = gen.int4_problem(M, K, G, seed=M * 31 + K + G)
-    check(run_int4(p, gpu), ref_int4(p), f"M={M} K={K} G={G}")
+    check(run_int4(p, gpu, path=path), ref_int4(p), f"M={M} K={K} G={G} path {path}")
 
 
 @pytest.mark.parametrize("batch", [2, 3, 4, 5, 8, 16])
@@ -92,20 +103,29 @@ def test_batched_valu(gpu, batch):
     check(run_int4(p, gpu, path=kq.PATH_VALU), ref_int4(p), f"valu batch {batch}")
 
 
-@pytest.mark.parametrize("rows,unroll", [(1, 1), (2, 1), (4, 1), (1, 2), (2, 2), (1, 4)])
-@pytest.mark.parametrize("K", [8192, 2880, 28672])
-def test_forced_launch_shapes_agree(gpu, rows, unroll, K):
-    """Every (rows per item, 64-chunk steps per item) shape gives the same
-    answer, including segment counts that do not divide the row."""
-    p = gen.int4_problem(1031, K, 64, seed=11 + K)
-    got = run_int4(p, gpu, path=kq.PATH_VALU, rows=rows, unroll=unroll)
-    check(got, ref_int4(p), f"rows={rows} unroll={unroll} K={K}")
+# (K parts, ring depth) per K: parts divide the 1 KiB steps of a row
+# (8192: 4 steps; 2880: 2 steps, the last one partial; 28672: 14 steps)
+VALU_PLANS = [(8192, 1, 2), (8192, 1, 8), (8192, 2, 4), (8192, 4, 2), (8192, 4, 8),
+              (2880, 1, 4), (2880, 2, 2), (2880, 2, 8),
+              (28672, 1, 8), (28672, 2, 4), (28672, 7, 2), (28672, 14, 8)]
 
 
-def test_forced_launch_shape_unsupported(gpu):
+@pytest.mark.parametrize("K,parts,depth", VALU_PLANS)
+@pytest.mark.parametrize("M,batch", [(1031, 1), (70, 2)])
+def test_forced_launch_shapes_agree(gpu, K, parts, depth, M, batch):
+    """Every (K parts, ring depth) plan of the vector path gives the oracle's
+    answer: split-K with the LDS reduction, padding items, a partial last
+    step (zero-padded x) and idle row lanes included."""
+    p = gen.int4_problem(M, K, 64, batch=batch, seed=11 + K + parts)
+    got = run_int4(p, gpu, path=kq.PATH_VALU, rows=parts, unroll=depth)
+    check(got, ref_int4(p), f"P={parts} D={depth} K={K} M={M} b={batch}")
+
+
+@pytest.mark.parametrize("parts,depth", [(3, 4), (1, 3)])
+def test_forced_launch_shape_unsupported(gpu, parts, depth):
     p = gen.int4_problem(64, 8192, 64, seed=1)
     with pytest.raises(kq.KQError) as e:
-        run_int4(p, gpu, path=kq.PATH_VALU, rows=4, unroll=4)  # 16 loads per buffer: too many
+        run_int4(p, gpu, path=kq.PATH_VALU, rows=parts, unroll=depth)  # 3 does not divide 4 steps
     assert e.value.status == kq.KQ_EUNSUPPORTED
 
 
@@ -137,10 +157,13 @@ def test_stream_read_runs(gpu):
 
 @pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 8, 9, 16])
 @pytest.mark.parametrize("M,K,G", [(4096, 4096, 64), (1031, 14336, 64), (777, 2944, 64),
-                                   (300, 8192, 128), (64, 28672, 64), (33, 1152, 128)])
+                                   (300, 8192, 128), (64, 28672, 64), (33, 1152, 128),
+                                   (513, 4096, 32), (100, 1024, 32)])
 def test_mfma_path(gpu, M, K, G, batch):
-    """Matrix-core path: split-K over 16 waves, rounds of 8 steps, LDS
-    reduction; batches past one LDS pass re-run over the token groups."""
+    """Matrix-core path: 16-row tiles, K split over the waves of a
+    workgroup and summed in LDS; G = 32 / 64 / 128 regroup the loaded words
+    with 4 / 2 / 0 lane swaps; batches past one LDS pass re-run over token
+    groups."""
     p = gen.int4_problem(M, K, G, batch=batch, seed=M + K + G + batch)
     check(run_int4(p, gpu, path=kq.PATH_MFMA), ref_int4(p), f"mfma M={M} K={K} G={G} b={batch}")
 
@@ -158,12 +181,30 @@ def test_mfma_layouts_bf16_fp32out(gpu, layout):
           "mfma bf16")
 
 
-@pytest.mark.parametrize("K,G", [(1024, 32), (2880, 64)])
+@pytest.mark.parametrize("K,G", [(1056, 32), (2880, 64)])
 def test_mfma_unsupported_falls_back(gpu, K, G):
-    """The matrix-core path needs G in {64, 128} and K % 128 == 0; forcing it
-    otherwise is refused, and the automatic choice uses the vector path."""
+    """The matrix-core path needs K % 128 == 0; forcing it otherwise is
+    refused, and the automatic choice uses the vector path."""
     p = gen.int4_problem(64, K, G, batch=8, seed=2)
     with pytest.raises(kq.KQError) as e:
         run_int4(p, gpu, path=kq.PATH_MFMA)
     assert e.value.status == kq.KQ_EUNSUPPORTED
     check(run_int4(p, gpu), ref_int4(p), f"auto path K={K} G={G}")
+
+
+@pytest.mark.parametrize("parts,depth", [(16, 2), (16, 8), (8, 4), (4, 2), (2, 8), (1, 4)])
+@pytest.mark.parametrize("M,batch", [(1000, 1), (257, 5)])
+def test_mfma_forced_plans_agree(gpu, parts, depth, M, batch):
+    """Every (K parts, ring depth) plan of the matrix-core path gives the
+    oracle's result: padding steps, idle tile lanes and several rounds per
+    workgroup included (K = 4096: 32 spans)."""
+    p = gen.int4_problem(M, 4096, 64, batch=batch, seed=parts * 10 + depth)
+    got = run_int4(p, gpu, path=kq.PATH_MFMA, rows=parts, unroll=depth)
+    check(got, ref_int4(p), f"mfma P={parts} D={depth} M={M} b={batch}")
+
+
+def test_mfma_forced_plan_unsupported(gpu):
+    p = gen.int4_problem(64, 4096, 64, seed=3)
+    with pytest.raises(kq.KQError) as e:
+        run_int4(p, gpu, path=kq.PATH_MFMA, rows=3, unroll=4)  # 3 does not divide 32 spans
+    assert e.value.status == kq.KQ_EUNSUPPORTED
