@@ -181,7 +181,7 @@ def bench_roofline(torch, kq, dev, timer, res):
     b = int4_bytes(M, K)
     res["roofline"] = {"bound": "hbm", "achieved": round(b / us / 1e3, 1), "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-                       "traffic": measured_traffic(), "kernel": "int4_gemv_valu (4096x14336, batch 1)",
+                       "traffic": measured_traffic(), "kernel": "int4_valu (vector path), 4096x14336, batch 1",
                        "bytes_per_launch": b, "us_per_launch": round(us, 3),
                        "launches_timed": reps * N_LAYERS}
     del layers

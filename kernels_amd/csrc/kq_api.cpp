@@ -60,11 +60,21 @@ kq_status run_int4(const uint32_t* W, const void* S, const void* B, kq_dtype sb_
     kq::Int4Cfg mcfg = forced ? *forced : kq::int4_mfma_default(M, K, batch);
     const bool valu_ok = kq::int4_valu_supported(K, batch, vcfg);
     const bool mfma_ok = kq::int4_mfma_supported(K, G, batch, mcfg);
-    // measured crossover (bench.py skinny sweep): the vector path streams 1 KiB
-    // rows and wins at 1-2 tokens; from 3 tokens (two vector passes) the
-    // matrix cores win
-    if (path == KQ_PATH_AUTO)
-        path = (mfma_ok && batch >= 3) || !valu_ok ? KQ_PATH_MFMA : KQ_PATH_VALU;
+    // Crossover measured with bench.py's skinny sweep: one matrix-core pass
+    // costs ~1.7 vector passes (64-byte row pieces per load instead of 1 KiB
+    // rows); a vector pass takes 2 tokens, a matrix-core pass as many as its
+    // LDS holds (all 16 at K = 4096, 2 at K = 28672). Take the fewer W reads.
+    if (path == KQ_PATH_AUTO) {
+        if (!mfma_ok) {
+            path = KQ_PATH_VALU;
+        } else if (!valu_ok) {
+            path = KQ_PATH_MFMA;
+        } else {
+            const uint32_t tpp = kq::int4_mfma_tokens_per_pass(M, K, G, batch, mcfg);
+            const uint32_t mp = tpp ? (batch + tpp - 1) / tpp : 1000, vp = (batch + 1) / 2;
+            path = 17 * mp < 10 * vp ? KQ_PATH_MFMA : KQ_PATH_VALU;
+        }
+    }
     if (path == KQ_PATH_VALU) {
         if (!valu_ok) return KQ_EUNSUPPORTED;
         return hip_status(kq::launch_int4_valu(W, Sp, Bp, mk, inter, X, Y, yf, M, K, G, batch, vcfg, s));

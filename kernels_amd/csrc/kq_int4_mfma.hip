@@ -69,6 +69,10 @@ uint32_t tokens_per_pass(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int
 
 }  // namespace
 
+uint32_t int4_mfma_tokens_per_pass(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg) {
+    return tokens_per_pass(M, K, G, batch, cfg);
+}
+
 Int4Cfg int4_mfma_default(uint32_t, uint32_t, uint32_t) { return Int4Cfg{0, 0}; }
 
 bool int4_mfma_supported(uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg) {

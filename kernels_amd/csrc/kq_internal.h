@@ -28,6 +28,8 @@ hipError_t launch_int4_mfma(const uint32_t* W, const uint16_t* S, const uint16_t
                             uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg, hipStream_t s);
 bool int4_mfma_supported(uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg);
 Int4Cfg int4_mfma_default(uint32_t M, uint32_t K, uint32_t batch);
+// Tokens one matrix-core pass stages in LDS (0: the shape is not supported).
+uint32_t int4_mfma_tokens_per_pass(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg);
 
 hipError_t launch_xsum32(const uint16_t* X, float* xs, uint32_t K, uint32_t batch, hipStream_t s);
 hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t s);
