@@ -152,11 +152,14 @@ typedef struct kq_moe_desc {
  * blob 14,024,704 B, offsets as in moe-fused/src/main.mm:23-25. */
 void kq_moe_default_desc(kq_moe_desc* d);
 
-/* Bytes of workspace the MoE entry points need for `batch` tokens (the
- * router logits). Its contents need no initialisation; kq_moe_workspace_init
- * zero-fills it (a kernel, not a memset, so it can sit in a captured graph).
- * Calls sharing one workspace must be stream-ordered. gate_up and down keep
- * their intermediates on chip and accept a NULL workspace. */
+/* Bytes of workspace the MoE entry points need for `batch` tokens: the router
+ * logits, a completion counter and the routing plan (distinct experts and
+ * their token slots) that the block's gate/up and down kernels read. A new
+ * workspace must be zeroed once with kq_moe_workspace_init (a kernel, not a
+ * memset, so it can sit in a captured graph) before its first use; every call
+ * leaves it ready for the next. Calls sharing one workspace must be
+ * stream-ordered. The standalone gate_up and down derive the plan from idx
+ * and accept a NULL workspace. */
 size_t kq_moe_workspace_size(const kq_moe_desc* d, uint32_t batch);
 kq_status kq_moe_workspace_init(void* ws, size_t bytes, kq_stream_t stream);
 

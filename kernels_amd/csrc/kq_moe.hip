@@ -2,34 +2,32 @@
 //
 // Reference: moe-fused/src/kernels.metal:98-265 (router_topk,
 // fused_gate_up_swiglu, fused_down_combine) and the block reference
-// moe-fused/src/main.mm:302-334. The block has two grid-wide dependencies
-// (the selected experts before the gather; all of h before down). On CDNA4
-// an in-kernel cross-workgroup handshake needs an agent-scope release, which
-// writes back the XCD's L2 -- far too slow for a few-microsecond block -- so
-// every dependency here is a kernel boundary and nothing inside a kernel
-// waits on another workgroup:
+// moe-fused/src/main.mm:302-334. Three launches, as in the reference:
 //
-// 1. moe_logits_k: router logits, one wave per expert reading its router row
-//    once for all tokens (fp32 accumulate), to the workspace; also half(x)
-//    when x is fp32 (router_topk writes xh the same way).
-// 2. moe_select_k (standalone router only): top-k + softmax per token.
-// 3. moe_gate_up_k: grid (16-row tile, u). Each workgroup derives the
-//    ascending list of distinct selected experts, takes the u-th and reads
-//    its gate/up rows once for every token slot that chose it. In the fused
-//    block each workgroup first runs top-k itself from the logits (a few
-//    hundred instructions, cheaper than a launch); workgroup (0,0) publishes
-//    idx/wgt. A half-wave (32 lanes) owns a gate row, the other half the
-//    matching up row (K = 2880 = 90 chunks -> 3 per lane), so SwiGLU happens
-//    on the two half-wave sums.
-// 4. moe_down_k: grid (8-row tile). A workgroup covers its rows for all
-//    selected experts (one wave per expert, looping), keeps per-slot
-//    wgt*(down.h + bias) in LDS and sums them in slot order: deterministic,
-//    no atomics.
+// 1. moe_router_k: router logits (one wave per expert, fp32 accumulation,
+//    every load issued before the first multiply), then the workgroup that
+//    completes last (a device-scope counter) runs top-k + softmax for every
+//    token and publishes idx, wgt and a plan: the ascending list of distinct
+//    selected experts and, per expert, the token slots that chose it. The
+//    logits travel through device-coherent stores and loads (relaxed
+//    agent-scope atomics: they bypass the non-coherent per-XCD L2), so no
+//    L2 write-back fence is needed -- measured ~2 us cheaper per block than a
+//    release fence, and cheaper than a separate selection launch.
+// 2. moe_gate_up_k: persistent workgroups take (expert, 2-row group) items
+//    from the plan; every workgroup stages the tokens' x in LDS once; a wave
+//    streams its items through a 2-deep ring of register slots (unconditional
+//    clamped loads, dequant at use), and each item is applied to every token
+//    slot that chose its expert -- so each selected expert's rows are read
+//    once per call. A half-wave owns the gate row, the other half the up row
+//    (K = 2880 = 90 chunks -> 3 per lane), so SwiGLU sees the two half sums.
+// 3. moe_down_k: a workgroup owns 8 output rows for every selected expert:
+//    (expert, 4-row) items in a 2-deep ring per wave, per-slot
+//    wgt * (down . h + bias) kept in LDS and summed in slot order --
+//    deterministic, no atomics.
 //
-// The activation a wave multiplies (x or h, per token slot) sits in its
-// registers as permuted fp16 pairs for all of the wave's rows; the weights
-// are dequantised with the AND-OR trick of kq_device.h; bf16 group scale and
-// bias apply once per 32-weight chunk.
+// Activations are used as permuted fp16 pairs with per-chunk sums (the
+// AND-OR dequant of kq_device.h); bf16 group scale and bias apply once per
+// 32-weight chunk.
 #include "kq_device.h"
 #include "kq_internal.h"
 
@@ -37,106 +35,126 @@ namespace kq {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kGuRows = 16;   // gate/up rows per workgroup (4 waves x 4 rows)
-constexpr int kGuRW = 4;      // gate/up rows per wave
-constexpr int kDnRows = 8;    // down rows per workgroup
-constexpr int kMaxSlots = 128;
+constexpr int kMaxSlots = 128;  // batch (16) x top_k (8)
 constexpr int kMaxTopK = 8;
+constexpr int kRtThreads = 256;  // router: 4 experts per workgroup
+constexpr int kGuThreads = 256;  // gate/up: 4 waves
+constexpr int kGuRW = 4;         // gate/up rows per wave
+constexpr int kGuRows = 16;      // gate/up rows per workgroup
+constexpr int kDnThreads = 256;  // down: 4 waves
+constexpr int kDnRows = 8;       // down rows per workgroup
 
+// Plan of one call: distinct selected experts (ascending) and their slots.
+struct Plan {
+    uint32_t n;
+    uint32_t pad[3];
+    uint32_t expert[kMaxSlots];
+    uint64_t mask[kMaxSlots][2];  // slot s: bit s of mask[.][0] (s < 64) or bit s-64 of [1]
+};
+
+// Workspace: [logits f32 batch x n_experts][completion counter][plan]
 struct WsLayout {
-    size_t lg, total;
+    size_t lg, cnt, plan, total;
 };
 
 WsLayout ws_layout(const kq_moe_desc& d, uint32_t batch) {
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
     WsLayout L;
     L.lg = 0;
-    L.total = al(L.lg + 4ull * batch * d.n_experts);
+    L.cnt = al(4ull * batch * d.n_experts);
+    L.plan = L.cnt + 256;
+    L.total = al(L.plan + sizeof(Plan));
     return L;
 }
 
-// ---------------------------------------------------------------------------
-// 1. router logits
-// ---------------------------------------------------------------------------
+// Eight consecutive elements as loaded (fp16: one u32x4; fp32: two f32x4).
 template <bool F32>
-__device__ __forceinline__ void load8(const void* p, size_t i, float v[8]) {
+struct Raw8;
+template <>
+struct Raw8<false> {
+    u32x4 v;
+};
+template <>
+struct Raw8<true> {
+    f32x4 a, b;
+};
+
+template <bool F32>
+__device__ __forceinline__ Raw8<F32> load8(const void* p, size_t i) {
+    Raw8<F32> r;
     if constexpr (F32) {
         const f32x4* q = reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(p) + i);
-        const f32x4 a = q[0], b = q[1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        r.a = q[0];
+        r.b = q[1];
     } else {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(p) + i);
-        v[0] = h2f(a.x & 0xFFFF); v[1] = h2f(a.x >> 16); v[2] = h2f(a.y & 0xFFFF); v[3] = h2f(a.y >> 16);
-        v[4] = h2f(a.z & 0xFFFF); v[5] = h2f(a.z >> 16); v[6] = h2f(a.w & 0xFFFF); v[7] = h2f(a.w >> 16);
+        r.v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(p) + i);
+    }
+    return r;
+}
+
+template <bool F32>
+__device__ __forceinline__ void unpack8(const Raw8<F32>& r, float v[8]) {
+    if constexpr (F32) {
+        v[0] = r.a.x; v[1] = r.a.y; v[2] = r.a.z; v[3] = r.a.w;
+        v[4] = r.b.x; v[5] = r.b.y; v[6] = r.b.z; v[7] = r.b.w;
+    } else {
+        v[0] = h2f(r.v.x & 0xFFFF); v[1] = h2f(r.v.x >> 16);
+        v[2] = h2f(r.v.y & 0xFFFF); v[3] = h2f(r.v.y >> 16);
+        v[4] = h2f(r.v.z & 0xFFFF); v[5] = h2f(r.v.z >> 16);
+        v[6] = h2f(r.v.w & 0xFFFF); v[7] = h2f(r.v.w >> 16);
     }
 }
 
-template <bool RF32, bool XF32>
-__global__ __launch_bounds__(kThreads) void moe_logits_k(const void* __restrict__ R,
-                                                         const void* __restrict__ X,
-                                                         uint32_t batch, uint32_t NE,
-                                                         uint32_t HID, uint16_t* __restrict__ xh,
-                                                         float* __restrict__ lg) {
-    constexpr int NBMAX = 16;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const uint32_t e = blockIdx.x * (kThreads / 64) + (tid >> 6);
-
-    if (XF32 && xh) {  // fp16 copy of x for the projections
-        const uint32_t tot = batch * HID;
-        for (uint32_t i = blockIdx.x * kThreads + tid; i < tot; i += gridDim.x * kThreads)
-            xh[i] = f2h(reinterpret_cast<const float*>(X)[i]);
+// Order key of a candidate: larger key = better. Selectable logits (not NaN,
+// not -inf) map to an order-preserving unsigned code in the high word (always
+// > 0; -0 counts as +0 so equal logits tie), unselectable ones to 0; the low
+// word is ~index, so among equal high words the lowest index is the largest.
+__device__ __forceinline__ uint64_t cand_key(float v, uint32_t e) {
+    uint32_t hi = 0;
+    if (v > -INFINITY) {
+        const uint32_t b = __builtin_bit_cast(uint32_t, v + 0.0f);
+        hi = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     }
-    if (e >= NE) return;
-    float acc[NBMAX];
-#pragma unroll
-    for (int t = 0; t < NBMAX; ++t) acc[t] = 0.0f;
-    for (uint32_t k = lane * 8; k < HID; k += 64 * 8) {
-        float r[8];
-        load8<RF32>(R, (size_t)e * HID + k, r);
-#pragma unroll
-        for (int t = 0; t < NBMAX; ++t) {
-            if ((uint32_t)t < batch) {
-                float x[8];
-                load8<XF32>(X, (size_t)t * HID + k, x);
-                float a = acc[t];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) a = fmaf(r[i], x[i], a);
-                acc[t] = a;
-            }
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < NBMAX; ++t) {
-        if ((uint32_t)t < batch) {
-            const float v = wave_sum(acc[t]);
-            if (lane == 0) lg[(size_t)t * NE + e] = v;
-        }
-    }
+    return ((uint64_t)hi << 32) | (uint32_t)~e;
 }
 
-// ---------------------------------------------------------------------------
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t k) {
+    const int lo = (int)(uint32_t)k, hi = (int)(uint32_t)(k >> 32);
+    const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROW_MASK, 0xF, false);
+    const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROW_MASK, 0xF, false);
+    const uint64_t o = ((uint64_t)ohi << 32) | olo;
+    return o > k ? o : k;
+}
+
+// Largest key of the wave, uniform (DPP butterfly, then lane 63).
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+    k = dpp_max_u64<0xB1, 0xF>(k);   // xor 1
+    k = dpp_max_u64<0x4E, 0xF>(k);   // xor 2
+    k = dpp_max_u64<0x124, 0xF>(k);  // row_ror 4
+    k = dpp_max_u64<0x128, 0xF>(k);  // row_ror 8
+    k = dpp_max_u64<0x142, 0xA>(k);  // row_bcast 15
+    k = dpp_max_u64<0x143, 0xC>(k);  // row_bcast 31
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)k, 63);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 63);
+    return ((uint64_t)hi << 32) | lo;
+}
+
 // top-k + softmax of one token, one wave (moe-fused/src/kernels.metal:149-162):
-// k passes of "strictly greater wins, ascending scan" -- ties go to the
-// lowest index, NaN and -inf are never selectable, and a pass with nothing
-// selectable picks expert 0 -- then softmax over the chosen logits.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ bool better(float va, uint32_t ia, float vb, uint32_t ib) {
-    const bool oka = va > -INFINITY, okb = vb > -INFINITY;
-    if (oka != okb) return oka;
-    if (!oka) return ia < ib;
-    return va > vb || (va == vb && ia < ib);
-}
-
-__device__ void topk_wave(const float* __restrict__ L, uint32_t NE, uint32_t TK,
+// k passes of "strictly greater wins, ascending scan" -- ties go to the lowest
+// index, NaN and -inf are never selectable, a pass with nothing selectable
+// picks expert 0 -- then softmax over the chosen logits. Up to 256 experts
+// (4 per lane); the passes are DPP reductions of cand_key, no LDS traffic.
+__device__ void topk_wave(const float* L, uint32_t NE, uint32_t TK,
                           uint32_t* idx_out, float* wgt_out) {
     const uint32_t lane = threadIdx.x & 63;
     float v[4];
+    uint64_t key[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t ei = lane + 64 * q;
-        v[q] = ei < NE ? L[ei] : -INFINITY;
+        v[q] = __hip_atomic_load(L + min(ei, NE - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        key[q] = ei < NE ? cand_key(v[q], ei) : 0;  // past NE: never the best (index ~ei > NE)
     }
     float chosen[kMaxTopK];
     uint32_t pick[kMaxTopK];
@@ -145,25 +163,26 @@ __device__ void topk_wave(const float* __restrict__ L, uint32_t NE, uint32_t TK,
         chosen[j] = -INFINITY;
         pick[j] = 0;
         if ((uint32_t)j < TK) {
+            uint64_t best = key[0];
+#pragma unroll
+            for (int q = 1; q < 4; ++q) best = key[q] > best ? key[q] : best;
+            best = wave_max_key(best);
+            uint32_t bi = ~(uint32_t)best;
             float bv = -INFINITY;
-            uint32_t bi = 0xFFFFFFFFu;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t ei = lane + 64 * q;
-                if (ei < NE && better(v[q], ei, bv, bi)) { bv = v[q]; bi = ei; }
+            if ((uint32_t)(best >> 32) == 0) {
+                bi = 0;  // nothing selectable
+            } else {
+                const uint32_t qb = (bi >> 6) & 3;  // uniform: select, no dynamic indexing
+                const float src = qb == 0 ? v[0] : qb == 1 ? v[1] : qb == 2 ? v[2] : v[3];
+                bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                   __builtin_bit_cast(int, src), bi & 63));
             }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o, 64);
-                const uint32_t oi = __shfl_xor(bi, o, 64);
-                if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-            }
-            if (!(bv > -INFINITY)) { bv = -INFINITY; bi = 0; }
             chosen[j] = bv;
             pick[j] = bi;
+            // the winner's logit becomes -inf (unselectable) for later passes
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                if (lane + 64 * q == bi) v[q] = -INFINITY;
+                if (lane + 64 * q == bi) key[q] = (uint64_t)(uint32_t)~bi;
         }
     }
     if (lane == 0) {
@@ -183,60 +202,130 @@ __device__ void topk_wave(const float* __restrict__ L, uint32_t NE, uint32_t TK,
     }
 }
 
-__global__ __launch_bounds__(kThreads) void moe_select_k(const float* __restrict__ lg,
-                                                         uint32_t batch, uint32_t NE,
-                                                         uint32_t TK, uint32_t* __restrict__ idx,
-                                                         float* __restrict__ wgt) {
-    for (uint32_t t = threadIdx.x >> 6; t < batch; t += kThreads / 64)
-        topk_wave(lg + (size_t)t * NE, NE, TK, idx + t * TK, wgt + t * TK);
-}
-
 // ---------------------------------------------------------------------------
-// Which expert a work item handles, and its token slots
+// 1. router logits + (last workgroup) top-k and plan
 // ---------------------------------------------------------------------------
-// Marks the experts selected by the slots in an LDS bitmap of 8 words.
-__device__ __forceinline__ void mark_experts(const uint32_t* idx, uint32_t nslots, uint32_t NE,
-                                             uint32_t* bits) {
-    const int tid = threadIdx.x;
+// Plan of the slots s_idx[0 .. nslots) into ps (all threads of the workgroup).
+__device__ void build_plan(const uint32_t* s_idx, uint32_t nslots, uint32_t NE, Plan& ps,
+                           uint32_t* bits) {
+    const uint32_t tid = threadIdx.x;
     if (tid < 8) bits[tid] = 0;
     __syncthreads();
-    if ((uint32_t)tid < nslots) {
-        const uint32_t e = min(idx[tid], NE - 1);
+    if (tid < nslots) {
+        const uint32_t e = min(s_idx[tid], NE - 1);
         atomicOr(&bits[e >> 5], 1u << (e & 31));
     }
     __syncthreads();
+    for (uint32_t e = tid; e < NE; e += blockDim.x) {
+        const uint32_t w = e >> 5, b = e & 31;
+        if (!((bits[w] >> b) & 1u)) continue;
+        uint32_t rank = __popc(bits[w] & ((1u << b) - 1u));
+        for (uint32_t i = 0; i < w; ++i) rank += __popc(bits[i]);
+        uint64_t m0 = 0, m1 = 0;
+        for (uint32_t s = 0; s < nslots; ++s)
+            if (min(s_idx[s], NE - 1) == e) {
+                if (s < 64) m0 |= 1ull << s;
+                else m1 |= 1ull << (s - 64);
+            }
+        ps.expert[rank] = e;
+        ps.mask[rank][0] = m0;
+        ps.mask[rank][1] = m1;
+    }
+    if (tid == 0) {
+        uint32_t n = 0;
+        for (int i = 0; i < 8; ++i) n += __popc(bits[i]);
+        ps.n = n;
+    }
+    __syncthreads();
 }
 
-struct Plan {
-    uint32_t e;         // expert id (valid if u < n_unique)
-    uint32_t n_unique;  // distinct experts selected
-    uint64_t m0, m1;    // slots s (s < 64: bit s of m0; else bit s-64 of m1)
-};
-
-// The u-th smallest marked expert and the slots that selected it (wave-level;
-// every lane of the wave must be active).
-__device__ Plan plan_for(const uint32_t* idx, uint32_t nslots, uint32_t NE, uint32_t u,
-                         const uint32_t* bits) {
-    const uint32_t lane = threadIdx.x & 63;
-    Plan p;
-    p.e = 0xFFFFFFFFu;
-    uint32_t cnt = 0;
+// Wave w of workgroup (x, y): expert 4x + w, tokens 2y, 2y + 1. Lane l takes
+// elements 8(l + 64i), i < IT (IT * 512 >= hidden); every router and x load
+// is issued before the first multiply (addresses clamped, results past the
+// row masked), so a wave pays one memory round trip.
+template <bool RF32, bool XF32, int IT>
+__global__ __launch_bounds__(kRtThreads) void moe_router_k(
+    const void* __restrict__ R, const void* __restrict__ X, uint32_t batch, uint32_t NE,
+    uint32_t HID, uint32_t TK, uint16_t* __restrict__ xh, float* lg, uint32_t* cnt,
+    uint32_t* __restrict__ idx_out, float* __restrict__ wgt_out, Plan* __restrict__ plan_out) {
+    constexpr int NBT = 2;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t e = blockIdx.x * (kRtThreads / 64) + wave, ec = min(e, NE - 1);
+    const uint32_t t0 = blockIdx.y * NBT;
+    Raw8<RF32> r[IT];
+    Raw8<XF32> x[NBT][IT];
 #pragma unroll
-    for (int w = 0; w < 8; ++w) {
-        uint32_t b = bits[w];
-        const uint32_t pc = __popc(b);
-        if (p.e == 0xFFFFFFFFu && u < cnt + pc) {
-            for (uint32_t i = 0; i < u - cnt; ++i) b &= b - 1;
-            p.e = w * 32 + __builtin_ctz(b);
-        }
-        cnt += pc;
+    for (int i = 0; i < IT; ++i) {
+        const uint32_t k = min((lane + 64 * i) * 8, HID - 8);
+        r[i] = load8<RF32>(R, (size_t)ec * HID + k);
+#pragma unroll
+        for (int t = 0; t < NBT; ++t)
+            x[t][i] = load8<XF32>(X, (size_t)min(t0 + t, batch - 1) * HID + k);
     }
-    p.n_unique = cnt;
-    const bool q0 = lane < nslots && min(idx[lane], NE - 1) == p.e;
-    const bool q1 = lane + 64 < nslots && min(idx[lane + 64], NE - 1) == p.e;
-    p.m0 = __ballot(q0);
-    p.m1 = __ballot(q1);
-    return p;
+    if (XF32 && xh) {  // fp16 copy of x for the projections, spread over the grid
+        const uint32_t tot = batch * HID, nthr = gridDim.x * gridDim.y * kRtThreads;
+        for (uint32_t i = (blockIdx.y * gridDim.x + blockIdx.x) * kRtThreads + tid; i < tot;
+             i += nthr)
+            xh[i] = f2h(reinterpret_cast<const float*>(X)[i]);
+    }
+    float acc[NBT] = {};
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+        if ((lane + 64 * i) * 8 < HID) {
+            float rv[8];
+            unpack8<RF32>(r[i], rv);
+#pragma unroll
+            for (int t = 0; t < NBT; ++t) {
+                float xv[8];
+                unpack8<XF32>(x[t][i], xv);
+                float a = acc[t];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) a = fmaf(rv[q], xv[q], a);
+                acc[t] = a;
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NBT; ++t) {
+        const float v = wave_sum(acc[t]);
+        if (lane == 0 && e < NE && t0 + t < batch)
+            __hip_atomic_store(lg + (size_t)(t0 + t) * NE + e, v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // this workgroup's logits have reached the device-coherent level before
+    // it is counted; the last one counted sees every logit
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ uint32_t s_last;
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 gridDim.x * gridDim.y - 1;
+    __syncthreads();
+    if (!s_last) return;
+
+    __shared__ uint32_t s_idx[kMaxSlots];
+    __shared__ float s_wgt[kMaxSlots];
+    __shared__ uint32_t bits[8];
+    __shared__ Plan ps;
+    for (uint32_t t = wave; t < batch; t += kRtThreads / 64)
+        topk_wave(lg + (size_t)t * NE, NE, TK, s_idx + t * TK, s_wgt + t * TK);
+    __syncthreads();
+    const uint32_t nslots = batch * TK;
+    if (tid < nslots) {
+        idx_out[tid] = s_idx[tid];
+        wgt_out[tid] = s_wgt[tid];
+    }
+    build_plan(s_idx, nslots, NE, ps, bits);
+    if (plan_out) {
+        const uint32_t n = ps.n;
+        if (tid == 0) plan_out->n = n;
+        for (uint32_t u = tid; u < n; u += kRtThreads) {
+            plan_out->expert[u] = ps.expert[u];
+            plan_out->mask[u][0] = ps.mask[u][0];
+            plan_out->mask[u][1] = ps.mask[u][1];
+        }
+    }
+    if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ uint32_t pop_slot(uint64_t& m0, uint64_t& m1) {
@@ -246,9 +335,6 @@ __device__ __forceinline__ uint32_t pop_slot(uint64_t& m0, uint64_t& m1) {
     return s;
 }
 
-// ---------------------------------------------------------------------------
-// register-resident activation: chunks c0 + 32j (j < J) of one fp16 vector
-// ---------------------------------------------------------------------------
 template <int J>
 struct Act {
     u32x4 p[J][4];   // permuted pairs of the chunk's 4 words
@@ -287,10 +373,18 @@ __device__ __forceinline__ void act_prep(const u32x4 (&raw)[J][4], Act<J>& a) {
 }
 
 // Load J chunks (lane c0 + 32j) of row m of a projection plus bf16 S|B.
+// Scale and bias stay as loaded (zero-extended halves) until the compute
+// uses them: combining them right after the load would make the wave wait
+// for every load in flight (vmcnt retires in order).
+template <int J>
+struct Row {
+    u32x4 w[J];
+    uint32_t s[J], b[J];
+};
+
 template <int J>
 __device__ __forceinline__ void load_row(const uint8_t* proj, const kq_moe_desc& d, uint32_t K,
-                                         uint32_t m, uint32_t c0, u32x4 (&w)[J],
-                                         uint32_t (&mt)[J]) {
+                                         uint32_t m, uint32_t c0, Row<J>& row) {
     const uint32_t nch = K >> 5, gpr = K >> 6;
     const u32x4* W = reinterpret_cast<const u32x4*>(proj + d.sub_w) + (size_t)m * nch;
     const uint16_t* S = reinterpret_cast<const uint16_t*>(proj + d.sub_s) + (size_t)m * gpr;
@@ -298,25 +392,32 @@ __device__ __forceinline__ void load_row(const uint8_t* proj, const kq_moe_desc&
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const uint32_t c = min(c0 + 32 * j, nch - 1);
-        w[j] = ldg_nt(W + c);
-        mt[j] = (uint32_t)S[c >> 1] | ((uint32_t)B[c >> 1] << 16);
+        row.w[j] = ldg_nt(W + c);
+        row.s[j] = S[c >> 1];
+        row.b[j] = B[c >> 1];
     }
 }
 
 // Per-lane partial dot of one row's J chunks with a register activation.
+// The rows stay in registers while a wave walks its token slots, so the
+// dequantisation is loop-invariant; the empty asm makes each chunk opaque at
+// its use, which keeps the compiler from hoisting the dequant of every row to
+// right after its load (a wait on every load, and ~200 registers of results).
 template <int J>
-__device__ __forceinline__ float row_dot(const u32x4 (&w)[J], const uint32_t (&mt)[J],
-                                         const Act<J>& a, uint32_t nch, uint32_t c0,
-                                         const DequantConsts& kc) {
+__device__ __forceinline__ float row_dot(const Row<J>& row, const Act<J>& a, uint32_t nch,
+                                         uint32_t c0, const DequantConsts& kc) {
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
+        u32x4 w = row.w[j];
+        uint32_t sr = row.s[j], br = row.b[j];
+        asm volatile("" : "+v"(w), "+v"(sr), "+v"(br));
         if (c0 + 32 * j < nch) {
-            float da = qdot8(w[j].x, a.p[j][0], 0.0f, kc);
-            float db = qdot8(w[j].y, a.p[j][1], 0.0f, kc);
-            da = qdot8(w[j].z, a.p[j][2], da, kc);
-            db = qdot8(w[j].w, a.p[j][3], db, kc);
-            const float s = bf2f(mt[j] & 0xFFFFu), b = bf2f(mt[j] >> 16);
+            float da = qdot8(w.x, a.p[j][0], 0.0f, kc);
+            float db = qdot8(w.y, a.p[j][1], 0.0f, kc);
+            da = qdot8(w.z, a.p[j][2], da, kc);
+            db = qdot8(w.w, a.p[j][3], db, kc);
+            const float s = bf2f((uint16_t)sr), b = bf2f((uint16_t)br);
             acc = fmaf(s, (da + db) - a.xc[j], fmaf(b, a.xs[j], acc));
         }
     }
@@ -324,73 +425,100 @@ __device__ __forceinline__ float row_dot(const u32x4 (&w)[J], const uint32_t (&m
 }
 
 // ---------------------------------------------------------------------------
-// 3. gather + gate + up + SwiGLU
+// plan and activations in LDS (gate/up and down)
 // ---------------------------------------------------------------------------
-template <int J, bool FROM_LOGITS>
-__global__ __launch_bounds__(kThreads) void moe_gate_up_k(
-    const uint8_t* __restrict__ pool, kq_moe_desc d, const uint32_t* __restrict__ idx_g,
-    float* __restrict__ wgt_pub, uint32_t* __restrict__ idx_pub, const float* __restrict__ lg,
-    const uint16_t* __restrict__ xh, uint16_t* __restrict__ H, uint32_t batch) {
-    __shared__ uint32_t bits[8];
-    __shared__ uint32_t s_idx[kMaxSlots];
-    __shared__ float s_wgt[kMaxSlots];
-    const uint32_t HID = d.hidden, IN = d.inter, TK = d.top_k;
-    const uint32_t nslots = batch * TK;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-
-    const uint32_t* idx = idx_g;
-    if constexpr (FROM_LOGITS) {
-        for (uint32_t t = wave; t < batch; t += kThreads / 64)
-            topk_wave(lg + (size_t)t * d.n_experts, d.n_experts, TK, s_idx + t * TK,
-                      s_wgt + t * TK);
-        __syncthreads();
-        if (blockIdx.x == 0 && blockIdx.y == 0 && (uint32_t)tid < nslots) {
-            idx_pub[tid] = s_idx[tid];  // for the down pass and the caller
-            wgt_pub[tid] = s_wgt[tid];
-        }
-        idx = s_idx;
+// Loads the plan (from the router) or builds it from idx; wgt to LDS if given.
+template <bool FROM_PLAN>
+__device__ void get_plan(const Plan* plan_g, const uint32_t* idx, const float* wgt,
+                         uint32_t nslots, uint32_t NE, Plan& ps, uint32_t* s_idx, float* s_wgt,
+                         uint32_t* bits) {
+    const uint32_t tid = threadIdx.x;
+    if (tid < nslots) {
+        s_idx[tid] = idx[tid];
+        if (wgt) s_wgt[tid] = wgt[tid];
     }
-    mark_experts(idx, nslots, d.n_experts, bits);
-    const Plan p = plan_for(idx, nslots, d.n_experts, blockIdx.y, bits);
-    if (blockIdx.y >= p.n_unique) return;
+    if constexpr (FROM_PLAN) {
+        const uint32_t n = plan_g->n;
+        if (tid == 0) ps.n = n;
+        for (uint32_t u = tid; u < n; u += blockDim.x) {
+            ps.expert[u] = plan_g->expert[u];
+            ps.mask[u][0] = plan_g->mask[u][0];
+            ps.mask[u][1] = plan_g->mask[u][1];
+        }
+        __syncthreads();
+    } else {
+        __syncthreads();
+        build_plan(s_idx, nslots, NE, ps, bits);
+    }
+}
 
-    const uint32_t half = lane >> 5, c0 = lane & 31, nch = HID >> 5;
-    const uint8_t* blob = pool + (size_t)p.e * d.blob;
+// ---------------------------------------------------------------------------
+// 2. gather + gate + up + SwiGLU
+// ---------------------------------------------------------------------------
+// Grid (16-row tile, u): workgroup (x, u) takes the u-th distinct selected
+// expert of the plan, wave w rows 16x + 4w .. +3, and issues every load it
+// needs at once (x of its first slot, 4 gate + 4 up rows, biases): one memory
+// round trip, with the whole matrix in flight over the grid. Each row group is
+// then applied to every token slot that chose the expert.
+template <int J, bool FROM_PLAN>
+__global__ __launch_bounds__(kGuThreads) void moe_gate_up_k(
+    const uint8_t* __restrict__ pool, kq_moe_desc d, const uint32_t* __restrict__ idx,
+    const Plan* __restrict__ plan_g, const uint16_t* __restrict__ xh, uint16_t* __restrict__ H,
+    uint32_t batch) {
+    const uint32_t HID = d.hidden, IN = d.inter, TK = d.top_k, nch = HID >> 5;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t half = lane >> 5, c0 = lane & 31, u = blockIdx.y;
+    uint32_t e, n;
+    uint64_t sm0, sm1;
+    if constexpr (FROM_PLAN) {
+        n = plan_g->n;
+        e = plan_g->expert[min(u, (uint32_t)kMaxSlots - 1)];
+        sm0 = plan_g->mask[u][0];
+        sm1 = plan_g->mask[u][1];
+    } else {
+        __shared__ Plan ps;
+        __shared__ uint32_t s_idx[kMaxSlots];
+        __shared__ float s_wgt[kMaxSlots];
+        __shared__ uint32_t bits[8];
+        get_plan<false>(nullptr, idx, nullptr, batch * TK, d.n_experts, ps, s_idx, s_wgt, bits);
+        n = ps.n;
+        e = ps.expert[u];
+        sm0 = ps.mask[u][0];
+        sm1 = ps.mask[u][1];
+    }
+    if (u >= n) return;
+    e = min(e, d.n_experts - 1);
+
+    const uint8_t* blob = pool + (size_t)e * d.blob;
     const uint8_t* proj = blob + (half ? d.off_up : d.off_gate);
     const uint32_t m0 = blockIdx.x * kGuRows + wave * kGuRW;
     const DequantConsts kc;
 
-    uint64_t sm0 = p.m0, sm1 = p.m1;
     uint32_t slot = pop_slot(sm0, sm1);
-    // x of the first slot ahead of the weights in the memory queue
     u32x4 raw[J][4];
     act_load<J>(xh + (size_t)(slot / TK) * HID, nch, c0, raw);
-
-    u32x4 w[kGuRW][J];
-    uint32_t mt[kGuRW][J];
+    Row<J> rows[kGuRW];
 #pragma unroll
-    for (int r = 0; r < kGuRW; ++r) load_row<J>(proj, d, HID, min(m0 + r, IN - 1), c0, w[r], mt[r]);
-    float bg = 0.0f, bu = 0.0f;
-    if (lane < kGuRW && m0 + lane < IN) {
-        bg = bf2f(reinterpret_cast<const uint16_t*>(blob + d.off_gate + d.sub_bi)[m0 + lane]);
-        bu = bf2f(reinterpret_cast<const uint16_t*>(blob + d.off_up + d.sub_bi)[m0 + lane]);
-    }
+    for (int r = 0; r < kGuRW; ++r) load_row<J>(proj, d, HID, min(m0 + r, IN - 1), c0, rows[r]);
+    const uint32_t brow = min(m0 + (lane & (kGuRW - 1)), IN - 1);
+    const uint32_t bg_raw = reinterpret_cast<const uint16_t*>(blob + d.off_gate + d.sub_bi)[brow];
+    const uint32_t bu_raw = reinterpret_cast<const uint16_t*>(blob + d.off_up + d.sub_bi)[brow];
 
     while (true) {
         Act<J> a;
         act_prep<J>(raw, a);
-        float g[kGuRW], u[kGuRW];
+        float g[kGuRW], up[kGuRW];
 #pragma unroll
         for (int r = 0; r < kGuRW; ++r) {
-            const float2 hs = half_sums(row_dot<J>(w[r], mt[r], a, nch, c0, kc));
+            const float2 hs = half_sums(row_dot<J>(rows[r], a, nch, c0, kc));
             g[r] = hs.x;
-            u[r] = hs.y;
+            up[r] = hs.y;
         }
 #pragma unroll
         for (int r = 0; r < kGuRW; ++r) {
-            if (lane == r && m0 + r < IN) {
-                const float gg = fminf(g[r] + bg, 7.0f);
-                const float uu = fminf(fmaxf(u[r] + bu, -7.0f), 7.0f);
+            if (lane == (uint32_t)r && m0 + r < IN) {
+                const float gg = fminf(g[r] + bf2f((uint16_t)bg_raw), 7.0f);
+                const float uu = fminf(fmaxf(up[r] + bf2f((uint16_t)bu_raw), -7.0f), 7.0f);
                 const float h = (gg / (1.0f + expf(-1.702f * gg))) * (uu + 1.0f);
                 H[(size_t)slot * IN + m0 + r] = f2h(h);
             }
@@ -402,78 +530,71 @@ __global__ __launch_bounds__(kThreads) void moe_gate_up_k(
 }
 
 // ---------------------------------------------------------------------------
-// 4. gather + down + weighted combine
+// 3. gather + down + weighted combine
 // ---------------------------------------------------------------------------
-template <int J>
-__global__ __launch_bounds__(kThreads) void moe_down_k(
+// ---------------------------------------------------------------------------
+// 3. gather + down + weighted combine
+// ---------------------------------------------------------------------------
+template <int J, bool FROM_PLAN>
+__global__ __launch_bounds__(kDnThreads) void moe_down_k(
     const uint8_t* __restrict__ pool, kq_moe_desc d, const uint32_t* __restrict__ idx,
-    const float* __restrict__ wgt, const uint16_t* __restrict__ H, void* __restrict__ Y,
-    int y_f32, uint32_t batch) {
-    __shared__ uint32_t bits[8];
+    const float* __restrict__ wgt, const Plan* __restrict__ plan_g,
+    const uint16_t* __restrict__ H, void* __restrict__ Y, int y_f32, uint32_t batch) {
+    __shared__ Plan ps;
     __shared__ uint32_t s_idx[kMaxSlots];
     __shared__ float s_wgt[kMaxSlots];
+    __shared__ uint32_t bits[8];
     __shared__ float ys[kMaxSlots][kDnRows];
-    const uint32_t HID = d.hidden, IN = d.inter, TK = d.top_k;
-    const uint32_t nslots = batch * TK;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if ((uint32_t)tid < nslots) {
-        s_idx[tid] = idx[tid];
-        s_wgt[tid] = wgt[tid];
-    }
-    mark_experts(s_idx, nslots, d.n_experts, bits);  // (its first barrier publishes s_idx)
-    const uint32_t half = lane >> 5, c0 = lane & 31, nch = IN >> 5;
+    constexpr int RP = kDnRows / 2;  // row pairs: lanes 0-31 row 2r, lanes 32-63 row 2r + 1
+    const uint32_t HID = d.hidden, IN = d.inter, TK = d.top_k, nslots = batch * TK;
+    const uint32_t nch = IN >> 5;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t half = lane >> 5, c0 = lane & 31;
     const uint32_t m0 = blockIdx.x * kDnRows;
-    constexpr int RP = kDnRows / 2;  // row pairs per wave
-    const DequantConsts kc;
-    uint32_t n_unique = 0;
-#pragma unroll
-    for (int wd = 0; wd < 8; ++wd) n_unique += __popc(bits[wd]);
 
-    // the distinct experts, one wave each (looping when there are more)
-    for (uint32_t u = wave; u < n_unique; u += kThreads / 64) {
-        const Plan p = plan_for(s_idx, nslots, d.n_experts, u, bits);
-        const uint8_t* proj = pool + (size_t)p.e * d.blob + d.off_down;
-        uint64_t sm0 = p.m0, sm1 = p.m1;
-        uint32_t slot = pop_slot(sm0, sm1);
+    get_plan<FROM_PLAN>(plan_g, idx, wgt, nslots, d.n_experts, ps, s_idx, s_wgt, bits);
+    const DequantConsts kc;
+    // a wave takes experts wave, wave + 4, ...: the first slot's h, then all
+    // the expert's rows of this workgroup, in one batch of loads
+    for (uint32_t u = wave; u < ps.n; u += kDnThreads / 64) {
+        const uint8_t* proj = pool + (size_t)ps.expert[u] * d.blob + d.off_down;
+        uint64_t sm0 = ps.mask[u][0], sm1 = ps.mask[u][1];
+        uint32_t s = pop_slot(sm0, sm1);
         u32x4 raw[J][4];
-        act_load<J>(H + (size_t)slot * IN, nch, c0, raw);
-        u32x4 w[RP][J];
-        uint32_t mt[RP][J];
+        act_load<J>(H + (size_t)s * IN, nch, c0, raw);
+        Row<J> rows[RP];
 #pragma unroll
         for (int r = 0; r < RP; ++r)
-            load_row<J>(proj, d, IN, min(m0 + 2 * r + half, HID - 1), c0, w[r], mt[r]);
-        float bi0 = 0.0f, bi1 = 0.0f;
-        if (lane < RP) {
-            const uint16_t* BI = reinterpret_cast<const uint16_t*>(proj + d.sub_bi);
-            bi0 = bf2f(BI[min(m0 + 2 * lane, HID - 1)]);
-            bi1 = bf2f(BI[min(m0 + 2 * lane + 1, HID - 1)]);
-        }
+            load_row<J>(proj, d, IN, min(m0 + 2 * r + half, HID - 1), c0, rows[r]);
+        const uint16_t* BI = reinterpret_cast<const uint16_t*>(proj + d.sub_bi);
+        const uint32_t br = m0 + 2 * (lane & (RP - 1));
+        const uint32_t b0 = BI[min(br, HID - 1)], b1 = BI[min(br + 1, HID - 1)];
         while (true) {
             Act<J> a;
             act_prep<J>(raw, a);
-            const float wt = s_wgt[slot];
+            const float wt = s_wgt[s];
             float2 hs[RP];
 #pragma unroll
-            for (int r = 0; r < RP; ++r) hs[r] = half_sums(row_dot<J>(w[r], mt[r], a, nch, c0, kc));
+            for (int r = 0; r < RP; ++r) hs[r] = half_sums(row_dot<J>(rows[r], a, nch, c0, kc));
 #pragma unroll
             for (int r = 0; r < RP; ++r) {
-                if (lane == r) {
-                    ys[slot][2 * r] = wt * (hs[r].x + bi0);
-                    ys[slot][2 * r + 1] = wt * (hs[r].y + bi1);
+                if (lane == (uint32_t)r) {
+                    ys[s][2 * r] = wt * (hs[r].x + bf2f((uint16_t)b0));
+                    ys[s][2 * r + 1] = wt * (hs[r].y + bf2f((uint16_t)b1));
                 }
             }
             if (!(sm0 | sm1)) break;
-            slot = pop_slot(sm0, sm1);
-            act_load<J>(H + (size_t)slot * IN, nch, c0, raw);
+            s = pop_slot(sm0, sm1);
+            act_load<J>(H + (size_t)s * IN, nch, c0, raw);
         }
     }
     __syncthreads();
     // combine in slot order (moe-fused/src/kernels.metal:254-263)
-    for (uint32_t i = tid; i < batch * kDnRows; i += kThreads) {
+    for (uint32_t i = tid; i < batch * kDnRows; i += kDnThreads) {
         const uint32_t t = i / kDnRows, r = i % kDnRows, m = m0 + r;
         if (m >= HID) continue;
         float acc = 0.0f;
-        for (uint32_t k = 0; k < TK; ++k) acc += ys[t * TK + k][r];
+        for (uint32_t q = 0; q < TK; ++q) acc += ys[t * TK + q][r];
         if (y_f32) reinterpret_cast<float*>(Y)[(size_t)t * HID + m] = acc;
         else reinterpret_cast<uint16_t*>(Y)[(size_t)t * HID + m] = f2h(acc);
     }
@@ -484,41 +605,77 @@ __global__ void fill_zero_k(uint32_t* p, size_t n) {
         p[i] = 0u;
 }
 
-uint32_t max_unique(const kq_moe_desc& d, uint32_t batch) {
-    const uint32_t n = batch * d.top_k;
-    return n < d.n_experts ? n : d.n_experts;
-}
-
 uint32_t chunks_j(uint32_t K) { return ((K >> 5) + 31) / 32; }
 
-hipError_t launch_logits(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
-                         const kq_moe_desc& d, uint16_t* xh, float* lg, hipStream_t s) {
-    const dim3 grid((d.n_experts + 3) / 4);
-#define KQ_LG(RF, XF)                                                                           \
-    moe_logits_k<RF, XF><<<grid, kThreads, 0, s>>>(R, X, batch, d.n_experts, d.hidden, xh, lg)
-    if (r_f32 && x_f32) KQ_LG(true, true);
-    else if (r_f32) KQ_LG(true, false);
-    else if (x_f32) KQ_LG(false, true);
-    else KQ_LG(false, false);
-#undef KQ_LG
+template <int IT>
+hipError_t launch_router_it(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
+                            const kq_moe_desc& d, uint16_t* xh, const WsLayout& L, uint8_t* ws,
+                            uint32_t* idx, float* wgt, hipStream_t s) {
+    const dim3 grid((d.n_experts + 3) / 4, (batch + 1) / 2);
+    float* lg = reinterpret_cast<float*>(ws + L.lg);
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
+    Plan* plan = reinterpret_cast<Plan*>(ws + L.plan);
+#define KQ_RT(RF, XF)                                                                     \
+    moe_router_k<RF, XF, IT><<<grid, kRtThreads, 0, s>>>(R, X, batch, d.n_experts, d.hidden, \
+                                                         d.top_k, xh, lg, cnt, idx, wgt, plan)
+    if (r_f32 && x_f32) KQ_RT(true, true);
+    else if (r_f32) KQ_RT(true, false);
+    else if (x_f32) KQ_RT(false, true);
+    else KQ_RT(false, false);
+#undef KQ_RT
     return hipGetLastError();
 }
 
-template <bool FL>
-hipError_t launch_gu(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx, float* wgt,
-                     uint32_t* idx_pub, const float* lg, const uint16_t* xh, uint16_t* H,
-                     uint32_t batch, hipStream_t s) {
-    const dim3 grid((d.inter + kGuRows - 1) / kGuRows, max_unique(d, batch));
-#define KQ_GU(JJ)                                                                               \
-    moe_gate_up_k<JJ, FL><<<grid, kThreads, 0, s>>>(pool, d, idx, wgt, idx_pub, lg, xh, H, batch)
+hipError_t launch_router(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
+                         const kq_moe_desc& d, uint16_t* xh, void* ws, uint32_t* idx, float* wgt,
+                         hipStream_t s) {
+    const WsLayout L = ws_layout(d, batch);
+    uint8_t* w = reinterpret_cast<uint8_t*>(ws);
+    const uint32_t it = (d.hidden + 511) / 512;  // hidden <= 4096 (validated)
+    if (it <= 2) return launch_router_it<2>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
+    if (it <= 4) return launch_router_it<4>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
+    if (it <= 6) return launch_router_it<6>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
+    return launch_router_it<8>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
+}
+
+template <int J, bool FP>
+hipError_t go_gu(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx, const Plan* plan,
+                 const uint16_t* xh, uint16_t* H, uint32_t batch, hipStream_t s) {
+    const uint32_t nslots = batch * d.top_k;
+    const dim3 grid((d.inter + kGuRows - 1) / kGuRows, nslots < d.n_experts ? nslots : d.n_experts);
+    moe_gate_up_k<J, FP><<<grid, kGuThreads, 0, s>>>(pool, d, idx, plan, xh, H, batch);
+    return hipGetLastError();
+}
+
+template <bool FP>
+hipError_t launch_gu(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
+                     const Plan* plan, const uint16_t* xh, uint16_t* H, uint32_t batch,
+                     hipStream_t s) {
     switch (chunks_j(d.hidden)) {
-        case 1: KQ_GU(1); break;
-        case 2: KQ_GU(2); break;
-        case 3: KQ_GU(3); break;
-        case 4: KQ_GU(4); break;
+        case 1: return go_gu<1, FP>(pool, d, idx, plan, xh, H, batch, s);
+        case 2: return go_gu<2, FP>(pool, d, idx, plan, xh, H, batch, s);
+        case 3: return go_gu<3, FP>(pool, d, idx, plan, xh, H, batch, s);
+        case 4: return go_gu<4, FP>(pool, d, idx, plan, xh, H, batch, s);
         default: return hipErrorInvalidValue;
     }
-#undef KQ_GU
+}
+
+template <bool FP>
+hipError_t launch_dn(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
+                     const float* wgt, const Plan* plan, const uint16_t* H, void* Y, bool y_f32,
+                     uint32_t batch, hipStream_t s) {
+    const dim3 grid((d.hidden + kDnRows - 1) / kDnRows);
+    const int yf = y_f32 ? 1 : 0;
+#define KQ_DN(JJ) \
+    moe_down_k<JJ, FP><<<grid, kDnThreads, 0, s>>>(pool, d, idx, wgt, plan, H, Y, yf, batch)
+    switch (chunks_j(d.inter)) {
+        case 1: KQ_DN(1); break;
+        case 2: KQ_DN(2); break;
+        case 3: KQ_DN(3); break;
+        case 4: KQ_DN(4); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef KQ_DN
     return hipGetLastError();
 }
 
@@ -538,46 +695,32 @@ hipError_t launch_ws_zero(void* ws, size_t bytes, hipStream_t s) {
 hipError_t launch_moe_router(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
                              const kq_moe_desc& d, uint32_t* idx, float* wgt, uint16_t* xh,
                              void* ws, hipStream_t s) {
-    float* lg = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + ws_layout(d, batch).lg);
-    hipError_t e = launch_logits(R, r_f32, X, x_f32, batch, d, xh, lg, s);
-    if (e != hipSuccess) return e;
-    moe_select_k<<<1, kThreads, 0, s>>>(lg, batch, d.n_experts, d.top_k, idx, wgt);
-    return hipGetLastError();
+    return launch_router(R, r_f32, X, x_f32, batch, d, xh, ws, idx, wgt, s);
 }
 
 hipError_t launch_moe_gate_up(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
                               const uint16_t* xh, uint16_t* H, uint32_t batch, hipStream_t s) {
-    return launch_gu<false>(pool, d, idx, nullptr, nullptr, nullptr, xh, H, batch, s);
+    return launch_gu<false>(pool, d, idx, nullptr, xh, H, batch, s);
 }
 
 hipError_t launch_moe_down(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
                            const float* wgt, const uint16_t* H, void* Y, bool y_f32,
                            uint32_t batch, hipStream_t s) {
-    const dim3 grid((d.hidden + kDnRows - 1) / kDnRows);
-    const int yf = y_f32 ? 1 : 0;
-#define KQ_DN(JJ) moe_down_k<JJ><<<grid, kThreads, 0, s>>>(pool, d, idx, wgt, H, Y, yf, batch)
-    switch (chunks_j(d.inter)) {
-        case 1: KQ_DN(1); break;
-        case 2: KQ_DN(2); break;
-        case 3: KQ_DN(3); break;
-        case 4: KQ_DN(4); break;
-        default: return hipErrorInvalidValue;
-    }
-#undef KQ_DN
-    return hipGetLastError();
+    return launch_dn<false>(pool, d, idx, wgt, nullptr, H, Y, y_f32, batch, s);
 }
 
 hipError_t launch_moe_block(const uint8_t* pool, const kq_moe_desc& d, const void* R, bool r_f32,
                             const void* X, bool x_f32, uint32_t batch, uint32_t* idx, float* wgt,
                             uint16_t* xh, uint16_t* H, void* Y, bool y_f32, void* ws,
                             hipStream_t s) {
-    float* lg = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + ws_layout(d, batch).lg);
-    hipError_t e = launch_logits(R, r_f32, X, x_f32, batch, d, xh, lg, s);
+    hipError_t e = launch_router(R, r_f32, X, x_f32, batch, d, xh, ws, idx, wgt, s);
     if (e != hipSuccess) return e;
+    const Plan* plan =
+        reinterpret_cast<const Plan*>(reinterpret_cast<const uint8_t*>(ws) + ws_layout(d, batch).plan);
     const uint16_t* xin = x_f32 ? xh : reinterpret_cast<const uint16_t*>(X);
-    e = launch_gu<true>(pool, d, nullptr, wgt, idx, lg, xin, H, batch, s);
+    e = launch_gu<true>(pool, d, idx, plan, xin, H, batch, s);
     if (e != hipSuccess) return e;
-    return launch_moe_down(pool, d, idx, wgt, H, Y, y_f32, batch, s);
+    return launch_dn<true>(pool, d, idx, wgt, plan, H, Y, y_f32, batch, s);
 }
 
 }  // namespace kq

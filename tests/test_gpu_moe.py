@@ -195,3 +195,42 @@ def test_block_fp32_inputs_and_fp16_out(gpu, pool16):
     got = to_f64(b.y)
     assert inf_rel(got, Yref) < 2e-3
     assert_close(got, Yref, atol=2e-2, rtol=2e-3, what="fp32-in block")
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_block_graph_replays(gpu, pool16, batch):
+    """The block captured in a HIP graph: every replay (with eager block calls
+    and synchronisations between replays, and the router's completion counter
+    carried in the workspace across all of them) equals the eager result bit
+    for bit -- the kernels are deterministic."""
+    host, pool = pool16
+    d = _pool_desc(16)
+    R, X = gen.moe_inputs(16, batch=batch, seed=70 + batch)
+    Rd, Xd = dev(R, gpu).view(torch.float16), dev(X, gpu).view(torch.float16)
+    b = Block(gpu, d, batch)
+
+    def block():
+        kq.moe_block(pool, d, Rd, Xd, b.idx, b.wgt, b.H, b.y, b.ws, b.wsb, batch=batch)
+
+    block()
+    torch.cuda.synchronize()
+    ref_idx, ref_y = b.idx.clone(), b.y.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        block()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        block()
+    for rep in range(4):
+        b.y.fill_(float("nan"))
+        b.idx.fill_(-1)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(b.idx, ref_idx), f"replay {rep} idx"
+        assert torch.equal(b.y, ref_y), f"replay {rep} y"
+        block()  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(b.y, ref_y), f"eager after replay {rep}"
