@@ -179,10 +179,10 @@ kq_status kq_vq_gemv(const uint8_t* IDX, const uint16_t* C, const uint16_t* S, c
     if (!IDX || !C || !S || !X || !Y) return KQ_ENULL;
     if (M == 0 || K == 0 || K % 32 || batch == 0 || batch > 16 || rows_per_cb == 0)
         return KQ_EINVAL;
-    if (K / 32 * 64 * 1ull > 60000) return KQ_EUNSUPPORTED;  // x must fit the LDS stage
     if (scale_group != K && (!pow2(scale_group) || scale_group < 32 || K % scale_group))
         return KQ_EINVAL;
     if (!(y_dtype == KQ_F16 || y_dtype == KQ_F32)) return KQ_EUNSUPPORTED;
+    if (!kq::vq_supported(M, K, rows_per_cb)) return KQ_EUNSUPPORTED;  // x must fit LDS
     if (!aligned(IDX, 16) || !aligned(X, 16) || !aligned(C, 4) || !aligned(S, 2)) return KQ_EALIGN;
     if (!aligned(Y, y_dtype == KQ_F32 ? 4 : 2)) return KQ_EALIGN;
     return hip_status(kq::launch_vq(IDX, C, S, X, Y, y_dtype == KQ_F32, M, K, rows_per_cb,

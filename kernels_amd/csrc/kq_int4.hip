@@ -55,10 +55,17 @@ struct VPlan {
     size_t lds;
 };
 
+template <int R, bool SB>
+struct VSlot;
 template <int R>
-struct VSlot {
+struct VSlot<R, true> {
     u32x4 w[R];
-    uint32_t s[R], b[R];  // interleaved: s holds (scale | bias << 16); else separate halves
+    uint32_t s[R];  // (scale | bias << 16)
+};
+template <int R>
+struct VSlot<R, false> {
+    u32x4 w[R];
+    uint16_t s[R], b[R];  // widened at use: a widening next to the load would wait for it
 };
 
 // The four fp16-pair operands of one packed word (see kq_device.h).
@@ -141,8 +148,8 @@ __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 2. prime the ring
-    VSlot<R> ring[D];
-    auto issue = [&](VSlot<R>& e, Cursor c) {
+    VSlot<R, SB> ring[D];
+    auto issue = [&](VSlot<R, SB>& e, Cursor c) {
         if (c.round >= A.rounds) {  // padding item: re-read the last real one
             c.round = A.rounds - 1;
             c.j = A.J - 1;
@@ -232,7 +239,7 @@ __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
             if (gq < A.groups_wg && gg < A.ngroups && row < A.M) store(row, rt % NB, v);
         }
     };
-    auto step = [&](const VSlot<R>& e, Cursor c, uint32_t n) {
+    auto step = [&](const VSlot<R, SB>& e, Cursor c, uint32_t n) {
         const uint32_t ch = (p * A.J + c.j) * 64 + lane;
 #pragma unroll
         for (int r = 0; r < R; ++r) {

@@ -83,6 +83,10 @@ template <int NG>
 struct Meta<NG, false> {  // NG scales and NG biases, two per dword
     uint32_t s[(NG + 1) / 2], b[(NG + 1) / 2];
 };
+template <>
+struct Meta<1, false> {  // one scale, one bias: kept 16-bit until use
+    uint16_t s[1], b[1];
+};
 
 template <int NG, bool SB>
 struct Slot {

@@ -34,6 +34,7 @@ uint32_t int4_mfma_tokens_per_pass(uint32_t M, uint32_t K, uint32_t G, uint32_t 
 hipError_t launch_xsum32(const uint16_t* X, float* xs, uint32_t K, uint32_t batch, hipStream_t s);
 hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t s);
 
+bool vq_supported(uint32_t M, uint32_t K, uint32_t rows_per_cb);
 hipError_t launch_vq(const uint8_t* IDX, const uint16_t* C, const uint16_t* S, const uint16_t* X,
                      void* Y, bool y_f32, uint32_t M, uint32_t K, uint32_t rows_per_cb,
                      uint32_t scale_group, uint32_t batch, hipStream_t s);

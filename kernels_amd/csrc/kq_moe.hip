@@ -379,7 +379,7 @@ __device__ __forceinline__ void act_prep(const u32x4 (&raw)[J][4], Act<J>& a) {
 template <int J>
 struct Row {
     u32x4 w[J];
-    uint32_t s[J], b[J];
+    uint16_t s[J], b[J];  // bf16 bits, widened at use
 };
 
 template <int J>

@@ -4,15 +4,21 @@
 //   w[m, 2i+t] = S[m, 2i/scale_group] * C[m/rows_per_cb][IDX[m,i]][t]
 // No bias and so no sum-of-x term (the codebook absorbs the group mean).
 //
-// Mapping on CDNA4:
-//   * the workgroup stages x (natural fp16 pairs, [token][word%4][chunk]
-//     layout for conflict-free ds_read_b128) and the codebook block(s) its
-//     rows need (256 x half2 = 1 KiB each) into LDS;
-//   * each wave owns R rows; lane l loads 16 indices (32 weights, one 16-byte
-//     global load) per 64-chunk step, U steps in flight;
-//   * each index byte addresses one half2 codeword in LDS (ds_read_b32), which
-//     is dotted with its activation pair by v_dot2_f32_f16 (fp32 accumulate);
-//   * the row scale applies once per 32-weight chunk (scale_group % 32 == 0).
+// Mapping on CDNA4 (the same skeleton as the int4 vector path, kq_int4.hip):
+//   * a wave instruction reads 1 KiB of indices of one row (lane l: the
+//     16-byte chunk 64*step + l = 16 indices = 32 weights);
+//   * the workgroup stages x once in LDS as its natural fp16 pairs (index i
+//     meets dword i of x) in [token][word%4][chunk] layout (conflict-free
+//     ds_read_b128; chunks past K zero-filled), and the codebook blocks of its
+//     rows (256 x half2 = 1 KiB each);
+//   * each index byte addresses one half2 codeword in LDS (ds_read_b32),
+//     dotted with its x pair by v_dot2_f32_f16 (fp32 accumulation); the
+//     lookups are shared by every token of the pass; the scale applies once
+//     per 32-weight chunk (scale_group % 32 == 0) or once per row;
+//   * a workgroup of P*Q waves owns contiguous row groups (R rows); wave (p, q)
+//     takes K-part p of row groups q, q+Q, ...; items stream through a 2-deep
+//     ring of register slots with unconditional clamped loads, the scale kept
+//     as loaded until its use (so a wave waits for one slot at a time).
 #include "kq_device.h"
 #include "kq_internal.h"
 
@@ -20,164 +26,372 @@ namespace kq {
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
+constexpr int kMaxWaves = 16;
+constexpr uint32_t kMaxNB = 4;  // tokens per pass
+constexpr size_t kLdsMax = 160 * 1024;
 
-template <int NB, int R, int U>
-__global__ __launch_bounds__(kThreads) void vq_gemv_k(
-    const uint8_t* __restrict__ IDX, const uint16_t* __restrict__ C,
-    const uint16_t* __restrict__ S, const uint16_t* __restrict__ X, void* __restrict__ Y,
-    int y_f32, uint32_t M, uint32_t K, uint32_t rpc, uint32_t sg_shift) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    const uint32_t nch = K >> 5, nw = K >> 3;
-    u32x4* xq = reinterpret_cast<u32x4*>(smem);                         // [NB][4][nch]
-    uint32_t* cb = reinterpret_cast<uint32_t*>(smem + (size_t)NB * nch * 64);  // [ncb][256]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t rows_per_block = kWaves * R;
-    const uint32_t mfirst = blockIdx.x * rows_per_block;
-    const uint32_t mlast = min(mfirst + rows_per_block, M) - 1;
-    const uint32_t cb0 = mfirst / rpc, ncb = mlast / rpc - cb0 + 1;
+struct QArgs {
+    const uint8_t* IDX;
+    const uint16_t* C;
+    const uint16_t* S;
+    const uint16_t* X;
+    void* Y;
+    uint32_t M, K, ntok, y_f32;
+    uint32_t nch, nchp, rpc, spr, cshift;  // chunks, padded chunks, rows per codebook,
+                                           // scales per row, chunk -> scale shift (31: per row)
+    uint32_t P, Q, J, groups_wg, ngroups, rounds, nreal, nsteps;
+    uint32_t cb_first_div;  // rows of a workgroup span at most this many codebooks
+};
 
-    for (uint32_t w = tid; w < NB * nw; w += kThreads) {
-        const uint32_t t = w / nw, wi = w - t * nw;
-        xq[(t * 4 + (wi & 3)) * nch + (wi >> 2)] =
-            *reinterpret_cast<const u32x4*>(X + (size_t)t * K + (size_t)wi * 8);
+struct QPlan {
+    uint32_t R, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, ncb;
+    size_t lds;
+};
+
+template <int R>
+struct QSlot {
+    u32x4 idx[R];
+    uint16_t sc[R];  // fp16 scale bits, as loaded (widened at use)
+};
+
+struct Cursor {
+    uint32_t j, round;
+    __device__ __forceinline__ void advance(uint32_t J) {
+        if (++j == J) {
+            j = 0;
+            ++round;
+        }
     }
-    for (uint32_t i = tid; i < ncb * 256; i += kThreads)
-        cb[i] = reinterpret_cast<const uint32_t*>(C)[(size_t)cb0 * 256 + i];
+};
+
+__host__ __device__ inline size_t qlds_x(uint32_t ntok, uint32_t nchp) {
+    return (size_t)ntok * nchp * 64;
+}
+
+// One index word (4 codeword lookups) dotted with its 4 x pairs.
+// (Replicating the 1 KiB codebook per lane to avoid random-index LDS bank
+// conflicts measured no faster: the kernel is bound by instruction issue --
+// extract, address, ds_read and dot2 per codeword -- not by bank conflicts.)
+__device__ __forceinline__ float vq_word(uint32_t word, u32x4 xv, const uint32_t* cbr, float acc) {
+    acc = dot2(cbr[word & 0xFF], xv.x, acc);
+    acc = dot2(cbr[(word >> 8) & 0xFF], xv.y, acc);
+    acc = dot2(cbr[(word >> 16) & 0xFF], xv.z, acc);
+    return dot2(cbr[word >> 24], xv.w, acc);
+}
+
+template <int NB, int R, int D>
+__global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const uint32_t nch = A.nch, nchp = A.nchp, nw = A.K >> 3;
+    u32x4* xp = reinterpret_cast<u32x4*>(smem);                                  // [NB][4][nchp]
+    uint32_t* cb = reinterpret_cast<uint32_t*>(smem + qlds_x(NB, nchp));          // [ncb][256]
+
+    const uint32_t tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & 63;
+    const uint32_t wave = tid >> 6, p = wave % A.P, q = wave / A.P;
+    const uint32_t g0 = blockIdx.x * A.groups_wg;
+    const uint32_t last_group = A.ngroups - 1, last_row = A.M - 1;
+    const uint32_t row_first = min(g0 * R, last_row);
+    const uint32_t cb0 = row_first / A.rpc;
+    const u32x4* I4 = reinterpret_cast<const u32x4*>(A.IDX);
+
+    // ---- 1. x loads first (vmcnt retires in order), then the ring
+    const uint32_t xtotal = NB * nw;
+    const u32x4* X4 = reinterpret_cast<const u32x4*>(A.X);
+    constexpr int kXr = 2;
+    u32x4 sv[kXr];
+    auto x_load = [&](uint32_t w0) {
+#pragma unroll
+        for (int r = 0; r < kXr; ++r) {
+            const uint32_t w = w0 + r * nthr + tid;
+            sv[r] = X4[w < xtotal ? w : xtotal - 1];
+        }
+    };
+    auto x_store = [&](uint32_t w0) {
+#pragma unroll
+        for (int r = 0; r < kXr; ++r) {
+            const uint32_t w = w0 + r * nthr + tid;
+            if (w < xtotal) {
+                const uint32_t t = w / nw, wi = w - t * nw;
+                xp[(t * 4 + (wi & 3)) * nchp + (wi >> 2)] = sv[r];
+            }
+        }
+    };
+    x_load(0);
+    // codebook blocks of this workgroup's rows (one dword per thread per round;
+    // at most 4 KiB, ahead of the weights like x)
+    const uint32_t ncb_total = (A.M + A.rpc - 1) / A.rpc;
+    const uint32_t ncb = min(A.cb_first_div, ncb_total - cb0), cbn = ncb * 256;
+    const uint32_t* Cw = reinterpret_cast<const uint32_t*>(A.C) + (size_t)cb0 * 256;
+    uint32_t cbv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t i = r * nthr + tid;
+        cbv[r] = Cw[i < cbn ? i : cbn - 1];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    QSlot<R> ring[D];
+    auto issue = [&](QSlot<R>& e, Cursor c) {
+        if (c.round >= A.rounds) {  // padding item: re-read the last real one
+            c.round = A.rounds - 1;
+            c.j = A.J - 1;
+        }
+        const uint32_t grp = min(g0 + c.round * A.Q + q, last_group);
+        const uint32_t ch = min((p * A.J + c.j) * 64 + lane, nch - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = min(grp * R + r, last_row);
+            e.idx[r] = ldg_nt(I4 + (size_t)row * nch + ch);
+            e.sc[r] = A.S[(size_t)row * A.spr + (A.cshift == 31 ? 0 : ch >> A.cshift)];
+        }
+    };
+    Cursor ci{0, 0};
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        issue(ring[d], ci);
+        ci.advance(A.J);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- 2. finish staging: x, zero padding, codebooks
+    x_store(0);
+    for (uint32_t w0 = kXr * nthr; w0 < xtotal; w0 += kXr * nthr) {
+        x_load(w0);
+        x_store(w0);
+    }
+    const uint32_t npad = nchp - nch;
+    for (uint32_t i = tid; i < NB * 4 * npad; i += nthr) {
+        const uint32_t tj = i / npad;
+        xp[tj * nchp + nch + (i - tj * npad)] = u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t i = r * nthr + tid;
+        if (i < cbn) cb[i] = cbv[r];
+    }
+    for (uint32_t i = 4 * nthr + tid; i < cbn; i += nthr) cb[i] = Cw[i];  // only if 4 * threads < entries
     __syncthreads();
 
-    const uint32_t row0 = mfirst + wave * R;
-    if (row0 >= M) return;
-    // sg_shift == 0 encodes one scale per row (scale_group == K)
-    const uint32_t spr = sg_shift ? K >> sg_shift : 1;   // scales per row
-    const uint32_t cshift = sg_shift ? sg_shift - 5 : 31; // chunk -> scale index
-
-    const u32x4* irow[R];
-    const uint16_t* srow[R];
-    const uint32_t* crow[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t m = min(row0 + r, M - 1);
-        irow[r] = reinterpret_cast<const u32x4*>(IDX + (size_t)m * (K >> 1));
-        srow[r] = S + (size_t)m * spr;
-        crow[r] = cb + (m / rpc - cb0) * 256;
-    }
     float acc[R][NB];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int t = 0; t < NB; ++t) acc[r][t] = 0.0f;
 
-    for (uint32_t it = 0; it < nch; it += 64 * U) {
-        u32x4 iv[U][R];
-        float sc[U][R];
+    auto finish = [&](uint32_t round) {
+        const uint32_t gl = round * A.Q + q, grp = g0 + gl;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (it + 64 * u < nch) {
-                const uint32_t c = min(it + 64 * u + lane, nch - 1);
+        for (int r = 0; r < R; ++r)
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    iv[u][r] = ldg_nt(irow[r] + c);
-                    sc[u][r] = h2f(srow[r][sg_shift ? (c >> cshift) : 0]);
+            for (int t = 0; t < NB; ++t) {
+                const float v = wave_sum(acc[r][t]);
+                acc[r][t] = 0.0f;
+                const uint32_t row = grp * R + r;
+                if (lane == 0 && gl < A.groups_wg && grp < A.ngroups && row < A.M) {
+                    const size_t o = (size_t)t * A.M + row;
+                    if (A.y_f32) reinterpret_cast<float*>(A.Y)[o] = v;
+                    else reinterpret_cast<uint16_t*>(A.Y)[o] = f2h(v);
                 }
             }
+    };
+    // P parts of a row meet in LDS (after the x stage, which stays live)
+    float* part = reinterpret_cast<float*>(cb + (size_t)A.cb_first_div * 256);  // [2][waves][R*NB]
+    auto finish_split = [&](uint32_t round) {
+        float* pw = part + ((size_t)(round & 1) * (A.P * A.Q) + wave) * (R * NB);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                const float v = wave_sum(acc[r][t]);
+                acc[r][t] = 0.0f;
+                if (lane == 0) pw[r * NB + t] = v;
+            }
+        __syncthreads();
+        const float* pr = part + (size_t)(round & 1) * (A.P * A.Q) * (R * NB);
+        for (uint32_t i = tid; i < A.Q * R * NB; i += nthr) {
+            const uint32_t qq = i / (R * NB), rt = i - qq * (R * NB);
+            float v = 0.0f;
+            for (uint32_t pp = 0; pp < A.P; ++pp) v += pr[(qq * A.P + pp) * (R * NB) + rt];
+            const uint32_t gq = round * A.Q + qq, gg = g0 + gq, row = gg * R + rt / NB;
+            if (gq < A.groups_wg && gg < A.ngroups && row < A.M) {
+                const size_t o = (size_t)(rt % NB) * A.M + row;
+                if (A.y_f32) reinterpret_cast<float*>(A.Y)[o] = v;
+                else reinterpret_cast<uint16_t*>(A.Y)[o] = f2h(v);
+            }
         }
+    };
+    auto step = [&](const QSlot<R>& e, Cursor c, uint32_t n) {
+        const uint32_t ch = (p * A.J + c.j) * 64 + lane;
+        const uint32_t grp = min(g0 + min(c.round, A.rounds - 1) * A.Q + q, last_group);
+        u32x4 xv[NB][4];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t c = it + 64 * u + lane;
-            if (it + 64 * u < nch && c < nch) {
+        for (int t = 0; t < NB; ++t)
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    // 16 codewords of this chunk, looked up once, reused per token
-                    uint32_t cw[16];
-                    const u32x4 v = iv[u][r];
+            for (int w = 0; w < 4; ++w) xv[t][w] = xp[(t * 4 + w) * nchp + ch];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const uint32_t word = q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w;
-                        cw[4 * q + 0] = crow[r][word & 0xFF];
-                        cw[4 * q + 1] = crow[r][(word >> 8) & 0xFF];
-                        cw[4 * q + 2] = crow[r][(word >> 16) & 0xFF];
-                        cw[4 * q + 3] = crow[r][word >> 24];
-                    }
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = min(grp * R + r, last_row);
+            const uint32_t blk = row / A.rpc - cb0;  // uniform
+            u32x4 iv = e.idx[r];
+            uint32_t sr = e.sc[r];
+            asm volatile("" : "+v"(iv), "+v"(sr));  // use the loaded values here, not earlier
+            const float sc = h2f((uint16_t)sr);
+            const uint32_t* cbr = cb + blk * 256;
 #pragma unroll
-                    for (int t = 0; t < NB; ++t) {
-                        float da = 0.0f, db = 0.0f;
+            for (int t = 0; t < NB; ++t) {
+                float da = vq_word(iv.x, xv[t][0], cbr, 0.0f);
+                float db = vq_word(iv.y, xv[t][1], cbr, 0.0f);
+                da = vq_word(iv.z, xv[t][2], cbr, da);
+                db = vq_word(iv.w, xv[t][3], cbr, db);
+                acc[r][t] = fmaf(sc, da + db, acc[r][t]);
+            }
+        }
+        if (n < A.nreal && c.j == A.J - 1) {
+            if (A.P == 1) finish(c.round);
+            else finish_split(c.round);
+        }
+    };
+
+    Cursor cc{0, 0};
+    uint32_t n = 0;
+    for (; n + D < A.nsteps; n += D) {
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            const u32x4 xv = xq[(t * 4 + q) * nch + c];  // x[32c+8q .. +7]
-                            da = dot2(cw[4 * q + 0], xv.x, da);
-                            db = dot2(cw[4 * q + 1], xv.y, db);
-                            da = dot2(cw[4 * q + 2], xv.z, da);
-                            db = dot2(cw[4 * q + 3], xv.w, db);
-                        }
-                        acc[r][t] = fmaf(sc[u][r], da + db, acc[r][t]);
-                    }
-                }
+        for (int d = 0; d < D; ++d) {
+            step(ring[d], cc, n + d);
+            cc.advance(A.J);
+            issue(ring[d], ci);
+            ci.advance(A.J);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        step(ring[d], cc, n + d);
+        cc.advance(A.J);
+    }
+}
+
+int g_vq_ncu = 0;
+uint32_t vq_ncu() {
+    if (g_vq_ncu <= 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            n > 0)
+            g_vq_ncu = n;
+        else
+            g_vq_ncu = 256;
+    }
+    return (uint32_t)g_vq_ncu;
+}
+
+// Plan as for the int4 vector path (kq_int4.hip, make_vplan): spread row
+// groups over every CU, no idle lanes, 2-deep ring; plus the codebook blocks a
+// workgroup's rows can touch.
+bool make_qplan(uint32_t M, uint32_t K, uint32_t ntok, uint32_t rpc, QPlan& out) {
+    const uint32_t nch = K >> 5, nstep = (nch + 63) / 64, nchp = nstep * 64, cu = vq_ncu();
+    bool found = false;
+    double best = 0.0;
+    for (uint32_t R = 2; R >= 1; --R) {
+        for (uint32_t P = 1; P <= kMaxWaves; ++P) {
+            if (nstep % P) continue;
+            const uint32_t D = 2;
+            const uint32_t ngroups = (M + R - 1) / R, J = nstep / P;
+            const uint32_t per_cu = (ngroups + cu - 1) / cu;
+            const uint32_t qmax = kMaxWaves / P;
+            const uint32_t rounds = (per_cu + qmax - 1) / qmax;
+            const uint32_t Q = (per_cu + rounds - 1) / rounds;
+            const uint32_t waves = P * Q, groups_wg = rounds * Q;
+            const uint32_t nwg = (ngroups + groups_wg - 1) / groups_wg;
+            const uint32_t nreal = rounds * J, nsteps = (nreal + D - 1) / D * D;
+            const uint32_t rows_wg = groups_wg * R;
+            const uint32_t ncb = (rows_wg - 1) / rpc + 2 < (M + rpc - 1) / rpc
+                                     ? (rows_wg - 1) / rpc + 2
+                                     : (M + rpc - 1) / rpc;
+            const size_t fixed = qlds_x(ntok, nchp) + (P > 1 ? (size_t)2 * waves * R * ntok * 4 : 0);
+            const size_t lds = fixed + (size_t)ncb * 1024;
+            if (lds > kLdsMax) continue;
+            double cost = (double)nsteps * waves * R;
+            if (waves < 8) cost *= 1.0 + 0.1 * (8 - waves);
+            if (P > 1) cost *= 1.02;
+            if (R == 2) cost *= 0.98;
+            if (!found || cost < best) {
+                found = true;
+                best = cost;
+                out = QPlan{R, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, ncb, lds};
             }
         }
     }
-
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int t = 0; t < NB; ++t) {
-            const float v = wave_sum(acc[r][t]);
-            if (lane == 0 && row0 + r < M) {
-                const size_t o = (size_t)t * M + row0 + r;
-                if (y_f32) reinterpret_cast<float*>(Y)[o] = v;
-                else reinterpret_cast<uint16_t*>(Y)[o] = f2h(v);
-            }
-        }
-}
-
-template <int NB, int R, int U>
-hipError_t vq_launch3(const uint8_t* IDX, const uint16_t* C, const uint16_t* S, const uint16_t* X,
-                      void* Y, bool y_f32, uint32_t M, uint32_t K, uint32_t rpc, uint32_t sgs,
-                      hipStream_t s) {
-    const uint32_t rpb = kWaves * R;
-    const uint32_t ncb_max = (rpb - 1) / rpc + 2;
-    const size_t lds = (size_t)NB * (K >> 5) * 64 + (size_t)ncb_max * 1024;
-    const dim3 grid((M + rpb - 1) / rpb);
-    vq_gemv_k<NB, R, U><<<grid, kThreads, lds, s>>>(IDX, C, S, X, Y, y_f32 ? 1 : 0, M, K, rpc, sgs);
-    return hipGetLastError();
+    return found;
 }
 
 template <int NB, int R>
-hipError_t vq_launch2(int U, const uint8_t* IDX, const uint16_t* C, const uint16_t* S,
-                      const uint16_t* X, void* Y, bool y_f32, uint32_t M, uint32_t K, uint32_t rpc,
-                      uint32_t sgs, hipStream_t s) {
-    switch (U) {
-        case 1: return vq_launch3<NB, R, 1>(IDX, C, S, X, Y, y_f32, M, K, rpc, sgs, s);
-        case 2: return vq_launch3<NB, R, 2>(IDX, C, S, X, Y, y_f32, M, K, rpc, sgs, s);
-        case 4: return vq_launch3<NB, R, 4>(IDX, C, S, X, Y, y_f32, M, K, rpc, sgs, s);
-        default: return vq_launch3<NB, R, 8>(IDX, C, S, X, Y, y_f32, M, K, rpc, sgs, s);
+hipError_t qgo(const QArgs& a, const QPlan& pl, hipStream_t s) {
+    auto kern = vq_valu<NB, R, 2>;
+    if (pl.lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)pl.lds);
+        if (e != hipSuccess) return e;
     }
+    kern<<<pl.nwg, pl.P * pl.Q * 64, pl.lds, s>>>(a);
+    return hipGetLastError();
+}
+
+template <int NB>
+hipError_t qgo_nb(const QArgs& a, const QPlan& pl, hipStream_t s) {
+    return pl.R == 2 ? qgo<NB, 2>(a, pl, s) : qgo<NB, 1>(a, pl, s);
 }
 
 }  // namespace
 
-size_t vq_lds_bytes(uint32_t K, uint32_t nb) { return (size_t)nb * (K >> 5) * 64 + 6 * 1024; }
+bool vq_supported(uint32_t M, uint32_t K, uint32_t rows_per_cb) {
+    QPlan pl;
+    return make_qplan(M, K, 1, rows_per_cb, pl);
+}
 
 hipError_t launch_vq(const uint8_t* IDX, const uint16_t* C, const uint16_t* S, const uint16_t* X,
                      void* Y, bool y_f32, uint32_t M, uint32_t K, uint32_t rows_per_cb,
                      uint32_t scale_group, uint32_t batch, hipStream_t s) {
-    uint32_t sgs = 0;  // 0: one scale per row
-    if (scale_group != K)
-        while ((1u << sgs) < scale_group) ++sgs;
-    const uint32_t steps = ((K >> 5) + 63) / 64;
-    const int U = steps <= 1 ? 1 : steps <= 2 ? 2 : steps <= 4 ? 4 : 8;
+    uint32_t sgs = 0;
+    while ((1u << sgs) < scale_group) ++sgs;
+    const bool per_row = scale_group == K;
     const size_t ysz = y_f32 ? 4 : 2;
-    // tokens in groups of 4, 2, 1 (each group one launch over the same rows)
     for (uint32_t t0 = 0; t0 < batch;) {
-        const uint32_t left = batch - t0;
-        const uint32_t nb = left >= 4 && vq_lds_bytes(K, 4) <= 65536 ? 4 : left >= 2 ? 2 : 1;
-        const uint16_t* Xt = X + (size_t)t0 * K;
-        void* Yt = reinterpret_cast<uint8_t*>(Y) + (size_t)t0 * M * ysz;
+        uint32_t nb = batch - t0 >= 4 ? 4 : batch - t0 >= 2 ? 2 : 1;
+        QPlan pl;
+        while (!make_qplan(M, K, nb, rows_per_cb, pl)) {
+            if (nb == 1) return hipErrorInvalidValue;
+            nb /= 2;
+        }
+        QArgs a;
+        a.IDX = IDX;
+        a.C = C;
+        a.S = S;
+        a.X = X + (size_t)t0 * K;
+        a.Y = reinterpret_cast<uint8_t*>(Y) + (size_t)t0 * M * ysz;
+        a.M = M;
+        a.K = K;
+        a.ntok = nb;
+        a.y_f32 = y_f32 ? 1 : 0;
+        a.nch = K >> 5;
+        a.nchp = ((K >> 5) + 63) / 64 * 64;
+        a.rpc = rows_per_cb;
+        a.spr = per_row ? 1 : K / scale_group;
+        a.cshift = per_row ? 31 : sgs - 5;
+        a.P = pl.P;
+        a.Q = pl.Q;
+        a.J = pl.J;
+        a.groups_wg = pl.groups_wg;
+        a.ngroups = (M + pl.R - 1) / pl.R;
+        a.rounds = pl.rounds;
+        a.nreal = pl.nreal;
+        a.nsteps = pl.nsteps;
+        a.cb_first_div = pl.ncb;
         hipError_t e;
-        if (nb == 4) e = vq_launch2<4, 1>(U, IDX, C, S, Xt, Yt, y_f32, M, K, rows_per_cb, sgs, s);
-        else if (nb == 2) e = vq_launch2<2, 1>(U, IDX, C, S, Xt, Yt, y_f32, M, K, rows_per_cb, sgs, s);
-        else e = vq_launch2<1, 1>(U, IDX, C, S, Xt, Yt, y_f32, M, K, rows_per_cb, sgs, s);
+        if (nb == 4) e = qgo_nb<4>(a, pl, s);
+        else if (nb == 2) e = qgo_nb<2>(a, pl, s);
+        else e = qgo_nb<1>(a, pl, s);
         if (e != hipSuccess) return e;
         t0 += nb;
     }
