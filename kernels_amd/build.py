@@ -16,7 +16,11 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB_DIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(LIB_DIR, "libkq.so")
+DRV_SRC = os.path.join(HERE, "drivers")
+BIN_DIR = os.path.join(HERE, "_bin")
+DRIVERS = ("int4gemv", "vqgemv", "moefused")
 ARCH = "gfx950"
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
@@ -45,6 +49,33 @@ def _compile(src, verbose):
     return obj, warn
 
 
+def _driver(name, verbose):
+    """The C++ host drivers: host-only code over the C ABI, linked against
+    libkq.so (found through an $ORIGIN-relative rpath) and the HIP runtime."""
+    out = os.path.join(BIN_DIR, name)
+    cmd = [os.path.join(ROCM, "llvm", "bin", "clang++"), "-O2", "-std=c++17", "-Wall", "-Wextra",
+           "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROOT, "include"),
+           "-I", os.path.join(ROCM, "include"), os.path.join(DRV_SRC, name + ".cpp"),
+           "-o", out + ".tmp", "-L", LIB_DIR, "-lkq", "-L", os.path.join(ROCM, "lib"),
+           "-lamdhip64", "-pthread", "-Wl,-rpath,$ORIGIN/../_lib",
+           "-Wl,-rpath," + os.path.join(ROCM, "lib")]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"driver build failed for {name}:\n{r.stdout}\n{r.stderr}")
+    if verbose and r.stderr.strip():
+        print(r.stderr, flush=True)
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def build_drivers(verbose: bool = False):
+    os.makedirs(BIN_DIR, exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=len(DRIVERS)) as ex:
+        return list(ex.map(lambda n: _driver(n, verbose), DRIVERS))
+
+
 def build(verbose: bool = False, jobs: int = 0) -> str:
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
@@ -62,6 +93,7 @@ def build(verbose: bool = False, jobs: int = 0) -> str:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
+    build_drivers(verbose)
     return LIB
 
 
