@@ -85,10 +85,12 @@ kq_status kq_int4_gemv_path(const uint32_t* W, const void* S, const void* B, kq_
                             kq_int4_path path, kq_stream_t stream);
 
 /* Tuning entry point: kq_int4_gemv with the kernel family and launch shape
- * forced. VALU: rows = rows per wave work item (1, 2, 4, 8), unroll = 64-chunk
- * steps per row held in registers (1, 2, 4, 8, 16; at least K/2048).
- * MFMA: rows = K parts P per workgroup (a divisor of K/128, at most 16),
- * unroll = ring depth D in 128-k spans (2, 4, 8); 0 = automatic for either.
+ * forced; 0 = automatic for either field.
+ * VALU: rows = K parts P per workgroup (a divisor of the number of 2048-k
+ * steps), unroll = ring depth D (2, 4, 8).
+ * MFMA: rows = K parts P per workgroup (a divisor of K/128; at most 8 with
+ * 4 tiles per wave, else 16), unroll = ring depth D (2; 3 with one tile per
+ * wave) or 10 * T + D with T the 16-row tiles per wave (1, 2, 4).
  * Returns KQ_EUNSUPPORTED for a shape the family cannot run. Used by the
  * benchmark sweeps and the tests. */
 kq_status kq_int4_gemv_cfg(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,

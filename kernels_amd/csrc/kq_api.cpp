@@ -59,11 +59,13 @@ kq_status run_int4(const uint32_t* W, const void* S, const void* B, kq_dtype sb_
     kq::Int4Cfg vcfg = forced ? *forced : kq::int4_valu_default(M, K, batch);
     kq::Int4Cfg mcfg = forced ? *forced : kq::int4_mfma_default(M, K, batch);
     const bool valu_ok = kq::int4_valu_supported(K, batch, vcfg);
-    const bool mfma_ok = kq::int4_mfma_supported(K, G, batch, mcfg);
-    // Crossover measured with bench.py's skinny sweep: one matrix-core pass
-    // costs ~1.7 vector passes (64-byte row pieces per load instead of 1 KiB
-    // rows); a vector pass takes 2 tokens, a matrix-core pass as many as its
-    // LDS holds (all 16 at K = 4096, 2 at K = 28672). Take the fewer W reads.
+    // the matrix-core path reads a span's separate scales / biases as one
+    // 4- or 8-byte word each
+    const bool meta_aligned = inter || (aligned(S, 8) && aligned(B, 8));
+    const bool mfma_ok = meta_aligned && kq::int4_mfma_supported(M, K, G, batch, mcfg);
+    // Crossover: a vector pass takes 2 tokens, the matrix-core pass all of
+    // them; one matrix-core pass costs ~1.7 vector passes (64-byte row pieces
+    // per load instead of 1 KiB rows). Take the fewer W reads.
     if (path == KQ_PATH_AUTO) {
         if (!mfma_ok) {
             path = KQ_PATH_VALU;

@@ -2,12 +2,14 @@
 // kernel is in kq_int4_mfma_kernel.h, instantiated per quant-group size in
 // kq_int4_mfma_g{32,64,128}.hip).
 //
-// A plan fixes the split of the 16 waves of a workgroup into P K-parts and
-// Q tile lanes (P divides the number of 128-k spans), the tiles per
-// workgroup (at most one workgroup per CU: ceil(tiles / CUs) tiles, in
-// rounds of Q), and the ring depth D. Among the P that fit the LDS, the plan
-// with the least per-workgroup work (waves x padded steps) wins; fewer than
-// 8 waves count as proportionally slower (too little in flight).
+// A plan fixes the tiles per wave T (4 with at most 8 waves per workgroup, 2
+// or 1 with at most 16: the register budget of T), the split of a
+// workgroup's waves into P K-parts (P divides the number of 128-k spans) and
+// Q row-group lanes (Q cut to the row groups a CU has), the row groups per
+// workgroup (in rounds of Q) and the ring depth D.
+// Cost = the busiest CU's weight bytes (workgroups it runs x waves x padded
+// steps x T), times a latency factor when a CU has less than ~48 KiB of loads
+// in flight. All tokens (up to 16) go in one pass.
 #include "kq_int4_mfma_kernel.h"
 
 namespace kq {
@@ -31,95 +33,100 @@ uint32_t ncu() {
 constexpr size_t kLdsMax = 160 * 1024;
 
 bool make_plan(uint32_t M, uint32_t K, uint32_t G, uint32_t ntok, Int4Cfg cfg, mfma::Plan& out) {
+    (void)ntok;
     const uint32_t nspan = K / 128, ntiles = (M + mfma::kTile - 1) / mfma::kTile, cu = ncu();
-    const uint32_t rmax = ntok == 1 ? 1 : 4;
-    if (cfg.unroll != 0 && cfg.unroll != 2 && cfg.unroll != 4 && cfg.unroll != 8) return false;
+    // cfg.unroll: 0 = automatic, D (2, 3) or 10 * T + D; cfg.rows: K parts P (0 = automatic)
+    uint32_t fT = 0, fD = 0;
+    if (cfg.unroll >= 10) {
+        fT = (uint32_t)cfg.unroll / 10;
+        fD = (uint32_t)cfg.unroll % 10;
+    } else if (cfg.unroll > 0) {
+        fD = (uint32_t)cfg.unroll;
+    }
+    if (fT && fT != 1 && fT != 2 && fT != 4) return false;
+    if (fD && fD != 2 && fD != 3) return false;
     bool found = false;
     double best = 0.0;
-    for (uint32_t P = mfma::kMaxWaves; P >= 1; --P) {
-        if (nspan % P) continue;
-        if (cfg.rows > 0 && (uint32_t)cfg.rows != P) continue;
-        const uint32_t Q = mfma::kMaxWaves / P, waves = P * Q, J = nspan / P;
-        const uint32_t per_cu = (ntiles + cu - 1) / cu;
-        const uint32_t rounds = (per_cu + Q - 1) / Q;
-        const uint32_t tiles_wg = rounds * Q;
-        const uint32_t nwg = (ntiles + tiles_wg - 1) / tiles_wg;
-        const uint32_t nreal = rounds * J;
-        const uint32_t D = cfg.unroll > 0 ? (uint32_t)cfg.unroll : nreal >= 8 ? 8 : nreal >= 4 ? 4 : 2;
-        const uint32_t nsteps = (nreal + D - 1) / D * D;
-        const size_t lds = mfma::lds_xp(ntok, K) + mfma::lds_xk(ntok, K, G) + mfma::lds_part(waves, rmax);
-        if (lds > kLdsMax) continue;
-        const double cost = (double)nsteps * waves * (waves < 8 ? 8.0 / waves : 1.0);
-        if (!found || cost < best) {
-            found = true;
-            best = cost;
-            out = mfma::Plan{P, Q, J, rounds, tiles_wg, nwg, nreal, nsteps, D, rmax, lds};
+    for (uint32_t T : {4u, 2u, 1u}) {
+        if (fT && T != fT) continue;
+        const uint32_t D = fD ? fD : 2;
+        if (D == 3 && T != 1) continue;
+        const uint32_t wmax = mfma::max_waves(G, T, D);
+        const uint32_t ngroups = (ntiles + T - 1) / T;
+        for (uint32_t P = 1; P <= wmax; ++P) {
+            if (nspan % P) continue;
+            if (cfg.rows > 0 && (uint32_t)cfg.rows != P) continue;
+            // Q is cut to the row groups a CU has (no idle lanes)
+            const uint32_t qmax = wmax / P, J = nspan / P;
+            const uint32_t per_cu = (ngroups + cu - 1) / cu;
+            const uint32_t rounds = (per_cu + qmax - 1) / qmax;
+            const uint32_t Q = (per_cu + rounds - 1) / rounds, waves = P * Q;
+            const uint32_t groups_wg = rounds * Q;
+            const uint32_t nwg = (ngroups + groups_wg - 1) / groups_wg;
+            const uint32_t nreal = rounds * J;
+            const uint32_t nsteps = (nreal + D - 1) / D * D;
+            const size_t lds = mfma::lds_part(waves, T, rounds, P);
+            if (lds > kLdsMax) continue;
+            const double inflight = (double)waves * D * T;  // KiB per CU
+            const double cost = (double)((nwg + cu - 1) / cu) * waves * nsteps * T *
+                                (inflight < 48.0 ? 48.0 / inflight : 1.0) * (P > 1 ? 1.02 : 1.0);
+            if (!found || cost < best) {
+                found = true;
+                best = cost;
+                out = mfma::Plan{T, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, waves, lds};
+            }
         }
     }
     return found;
 }
 
-// Most tokens (<= 16) one pass can stage.
-uint32_t tokens_per_pass(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg) {
-    mfma::Plan pl;
-    for (uint32_t t = batch < 16 ? batch : 16; t >= 1; --t)
-        if (make_plan(M, K, G, t, cfg, pl)) return t;
-    return 0;
-}
-
 }  // namespace
 
 uint32_t int4_mfma_tokens_per_pass(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg) {
-    return tokens_per_pass(M, K, G, batch, cfg);
+    mfma::Plan pl;
+    return int4_mfma_supported(M, K, G, batch, cfg) && make_plan(M, K, G, batch, cfg, pl) ? batch : 0;
 }
 
 Int4Cfg int4_mfma_default(uint32_t, uint32_t, uint32_t) { return Int4Cfg{0, 0}; }
 
-bool int4_mfma_supported(uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg) {
-    if (batch < 1 || batch > 16) return false;
+// Buffer loads address with 32-bit offsets: W, the scales and x must each
+// span less than 2 GiB.
+bool int4_mfma_supported(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg) {
+    if (batch < 1 || batch > 16 || M == 0) return false;
     if (!(G == 32 || G == 64 || G == 128) || K % 128) return false;
-    return tokens_per_pass(16, K, G, 1, cfg) >= 1;
+    if ((uint64_t)M * K / 2 >= (1ull << 31)) return false;
+    mfma::Plan pl;
+    return make_plan(M, K, G, batch, cfg, pl);
 }
 
 hipError_t launch_int4_mfma(const uint32_t* W, const uint16_t* S, const uint16_t* B, int meta_kind,
                             bool interleaved, const uint16_t* X, void* Y, bool y_f32, uint32_t M,
                             uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg, hipStream_t s) {
-    const uint32_t per_pass = tokens_per_pass(M, K, G, batch, cfg);
-    if (per_pass == 0) return hipErrorInvalidValue;
-    const size_t ysz = y_f32 ? 4 : 2;
-    for (uint32_t t0 = 0; t0 < batch;) {
-        const uint32_t nt = batch - t0 < per_pass ? batch - t0 : per_pass;
-        mfma::Plan pl;
-        if (!make_plan(M, K, G, nt, cfg, pl)) return hipErrorInvalidValue;
-        mfma::Args a;
-        a.W = W;
-        a.S = S;
-        a.B = B;
-        a.X = X + (size_t)t0 * K;
-        a.Y = reinterpret_cast<uint8_t*>(Y) + (size_t)t0 * M * ysz;
-        a.M = M;
-        a.K = K;
-        a.ntok = nt;
-        a.y_f32 = y_f32 ? 1 : 0;
-        a.nspan = K / 128;
-        a.gpr = K / G;
-        a.P = pl.P;
-        a.Q = pl.Q;
-        a.J = pl.J;
-        a.tiles_wg = pl.tiles_wg;
-        a.ntiles = (M + mfma::kTile - 1) / mfma::kTile;
-        a.rounds = pl.rounds;
-        a.nreal = pl.nreal;
-        a.nsteps = pl.nsteps;
-        const bool bf = meta_kind == 1;
-        hipError_t e;
-        if (G == 32) e = launch_mfma_g32(a, pl, interleaved, bf, s);
-        else if (G == 64) e = launch_mfma_g64(a, pl, interleaved, bf, s);
-        else e = launch_mfma_g128(a, pl, interleaved, bf, s);
-        if (e != hipSuccess) return e;
-        t0 += nt;
-    }
-    return hipSuccess;
+    mfma::Plan pl;
+    if (!make_plan(M, K, G, batch, cfg, pl)) return hipErrorInvalidValue;
+    mfma::Args a;
+    a.W = W;
+    a.S = S;
+    a.B = B;
+    a.X = X;
+    a.Y = Y;
+    a.M = M;
+    a.K = K;
+    a.ntok = batch;
+    a.y_f32 = y_f32 ? 1 : 0;
+    a.gpr = K / G;
+    a.P = pl.P;
+    a.Q = pl.Q;
+    a.J = pl.J;
+    a.ngroups = ((M + mfma::kTile - 1) / mfma::kTile + pl.T - 1) / pl.T;
+    a.groups_wg = pl.groups_wg;
+    a.rounds = pl.rounds;
+    a.nreal = pl.nreal;
+    a.nsteps = pl.nsteps;
+    const bool bf = meta_kind == 1;
+    if (G == 32) return launch_mfma_g32(a, pl, interleaved, bf, s);
+    if (G == 64) return launch_mfma_g64(a, pl, interleaved, bf, s);
+    return launch_mfma_g128(a, pl, interleaved, bf, s);
 }
 
 }  // namespace kq

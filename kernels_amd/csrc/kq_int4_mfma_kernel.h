@@ -1,46 +1,56 @@
-// kq_int4_mfma_kernel.h -- int4 group-affine GEMV / skinny GEMM (batch <= 16)
-// on the gfx950 matrix cores (v_mfma_f32_16x16x32_f16). Instantiated per
-// quant-group size in kq_int4_mfma_g{32,64,128}.hip (compiled in parallel).
+// kq_int4_mfma_kernel.h -- int4 group-affine skinny GEMM (1 to 16 tokens in
+// one pass) on the gfx950 matrix cores. Instantiated per quant-group size in
+// kq_int4_mfma_g{32,64,128}.hip (compiled in parallel).
 //
 // Math (reference: int4-gemv/src/kernels.metal:17-31, 397-448):
-//   y[b,m] = sum_g S[m,g] * (q[m,g,:] . x[b,g,:]) + B[m,g] * sum(x[b,g,:])
+//   y[t,m] = sum_g S[m,g] * (q[m,g,:] . x[t,g,:]) + B[m,g] * sum(x[t,g,:])
 // Nibbles become fp16 by AND-OR into fp16 exponents (kq_device.h): a word
-// gives (1024+n0,1024+n4)(64+n1,64+n5)(1024+n2,1024+n6)(64+n3,64+n7), so one
-// word costs 1 shift + 4 AND-OR and the multiply-accumulate runs on the
-// matrix pipe; the constant xc = 1024*sum(x_even) + 64*sum(x_odd) of a group
-// is subtracted once per group in the epilogue acc += s*(D - xc) + b*xs.
+// gives the eight values magic_k + q_k (magic 1024 or 64 by nibble parity),
+// exact in fp16. Per quant group g the matrix cores form
+//   Dg[t,m] = sum_{k in g} (magic_k + q_k) x[t,k]                (v_mfma 16x16x32 f16)
+// and the epilogue is
+//   acc[t,m] += S[m,g] * Dg[t,m]                                (VALU, 1 FMA per value)
+//            +  sum_g ( B[m,g] * xs[t,g] + S[m,g] * xn[t,g] )    (v_mfma 16x16x4 f32)
+// with xs = sum_{k in g} x_k and xn = -sum_{k in g} magic_k x_k. All products
+// are exact in fp32 and every sum is an fp32 sum.
 //
-// MFMA operands (D = A.B + C; A 16x32, B 32x16, measured lane layout):
-//   A = x: lane l holds token l%16, 8 k of lane group g = l/16
-//   B = W: lane l holds row   l%16, 8 k of lane group g     (one packed word)
-//   D:     lane l holds tokens 4g+r (r < 4) of row l%16.
-// Tokens beyond the batch hold zeros in A (their lanes never read x).
+// xs and xn depend on x only. They come from one more f16 MFMA per 32 k whose
+// A operand is a constant matrix (row 8w+p = ones over group 2p+w, row
+// 8w+4+p = -magic over the same group, other rows zero) and whose B operand is
+// the x registers the main MFMAs already hold. Its result lands with lane L
+// holding, in register p, sum-row 4(L/16)+p of token L%16 -- exactly the A
+// operand layout of v_mfma_f32_16x16x4_f32 (lane L: A[L%16][L/16]). So
+// register p is the A operand of the correction MFMA for group pair p, whose
+// B operand is (B, S, B', S') of the pair's two groups for row L%16 at k =
+// L/16. No lane exchange is needed.
 //
-// Memory: a lane loads 16 B = words 4g..4g+3 of a 128-k "span" of its row,
-// i.e. a wave instruction reads 64 B from each of 16 rows, and a wave streams
-// consecutive spans of the same rows. Register j of lane group g then holds
-// word 4g+j. For the per-group epilogue every MFMA's 32 k must lie in one
-// quant group, which v_permlane{32,16}_swap arrange:
-//   G = 128: one group per span, no exchange; MFMA j uses words 4g+j.
-//   G = 64:  swap (r0,r2), (r1,r3) between lanes 0-31 and 32-63; registers
-//            0,1 then hold group A (words 0-7), registers 2,3 group B.
-//   G = 32:  a 4x4 transpose (the G = 64 swap, then permlane16 swaps of
-//            (r0,r1), (r2,r3)); register j holds word 4j+g = group j.
-// x is staged once per workgroup in LDS as permuted fp16 pairs, and each
-// lane reads the words matching its (exchanged) registers.
+// MFMA operand layouts (D = A.B + C, measured):
+//   16x16x32 f16: A lane L = row L%16, 8 k of group L/16; B lane L = column
+//                 L%16, 8 k of group L/16; D lane L = rows 4(L/16)+r, col L%16.
+//   x is A (rows = tokens), W is B (columns = weight rows), so D lane L holds
+//   tokens 4(L/16)+r of weight row L%16; the accumulators keep that layout.
 //
-// Work split: a 16-row tile is the unit of rows. A workgroup of P*Q waves
-// owns a contiguous range of tiles; wave (p, q) takes K-part p (J = nspan/P
-// consecutive spans) of tile q, q+Q, ... ("rounds"), and the P partial tiles
-// of a round are summed in LDS in a fixed order (deterministic).
+// Memory: a lane loads 16 B (a 128-k "span" has 16 words per row; lane group
+// L/16 takes words 4(L/16)..+3), so one wave instruction reads 64 B from each
+// of 16 rows. A wave owns T row tiles (16T rows) and one K part; per span it
+// loads the T tiles' words and scale/bias, and x of the span (four 16-B loads
+// per lane, L1/L2-resident, permuted in registers to the dequant order). All
+// loads are buffer loads: the lane-constant part of an address sits in a VGPR
+// and the span offset in an SGPR, so addressing costs no vector instructions.
+// For the per-group epilogue each MFMA's 32 k must lie in one quant group;
+// v_permlane{32,16}_swap arrange that (G = 64: swap (r0,r2), (r1,r3) between
+// the wave halves; G = 32: then permlane16 swaps of (r0,r1), (r2,r3)).
 //
-// Pipelining: each wave streams its (tile, span) steps through a ring of D
-// register buffers. Every load is unconditional (out-of-range rows and steps
-// are clamped to valid addresses and their results discarded) and is first
-// used by the compute of its own step, so the waitcnt pass sees one straight
-// sequence and waits for exactly one buffer at a time (vmcnt = loads of the
-// other D-1 buffers). A branch around a load, or a use of loaded data right
-// after the load, would make it wait for everything in flight.
+// Work split: a workgroup of P*Q waves owns groups_wg consecutive row groups
+// (T tiles each); wave (p, q) takes K part p (J spans) of row groups q, q+Q,
+// ... ("rounds"). The P partial tiles of a round are summed in LDS in a fixed
+// order (deterministic).
+//
+// Pipelining: each wave streams its (row group, span) steps through a ring of
+// D register slots. Every load is unconditional (rows past the end and
+// padding steps are clamped to valid addresses, their results discarded) and
+// is first used by the compute of its own step, so the waitcnt pass sees one
+// straight sequence and waits for exactly one slot at a time.
 #pragma once
 #include "kq_device.h"
 #include "kq_internal.h"
@@ -48,7 +58,6 @@
 namespace kq {
 namespace mfma {
 
-constexpr int kMaxWaves = 16;
 constexpr int kTile = 16;
 
 struct Args {
@@ -58,91 +67,130 @@ struct Args {
     const uint16_t* X;  // [ntok][K] fp16
     void* Y;            // [ntok][M]
     uint32_t M, K, ntok, y_f32;
-    uint32_t nspan, gpr;     // 128-k spans and quant groups per row
-    uint32_t P, Q, J;        // K parts, tile lanes, spans per part
-    uint32_t tiles_wg;       // tiles per workgroup (= rounds * Q)
-    uint32_t ntiles;         // tiles in total
-    uint32_t rounds;         // rounds per workgroup
-    uint32_t nreal, nsteps;  // steps per wave (rounds * J) and padded to D
+    uint32_t gpr;                // quant groups per row
+    uint32_t P, Q, J;            // K parts, row-group lanes, spans per part
+    uint32_t ngroups;            // row groups (T tiles each) in total
+    uint32_t groups_wg, rounds;  // row groups per workgroup (= rounds * Q)
+    uint32_t nreal, nsteps;      // steps per wave (rounds * J), padded to D
 };
 
 // Launch plan chosen on the host.
 struct Plan {
-    uint32_t P, Q, J, rounds, tiles_wg, nwg, nreal, nsteps, D, rmax;
+    uint32_t T, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, waves;
     size_t lds;
 };
 
-// Scale/bias registers of one span (NG groups) as loaded, converted at use.
+// Waves per workgroup that the register budget of (G, T, D) allows without
+// spills: 16 waves leave 128 registers per lane, 8 leave 256.
+__host__ __device__ constexpr uint32_t max_waves(uint32_t G, uint32_t T, uint32_t D) {
+    return T == 4 ? 8 : (G == 32 && (T == 2 || D == 3)) ? 8 : 16;
+}
+
+__host__ __device__ inline size_t lds_part(uint32_t waves, uint32_t T, uint32_t rounds, uint32_t P) {
+    return P > 1 ? (size_t)(rounds > 1 ? 2 : 1) * waves * T * 4 * 64 * 4 : 0;
+}
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// Raw buffer descriptor (stride 0; word 3 = gfx9 default data format).
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+constexpr int kNT = 2;  // cache policy of streamed weights: non-temporal
+
+// Scale/bias registers of one span (NG groups), converted at use.
 template <int NG, bool SB>
 struct Meta;
-template <int NG>
-struct Meta<NG, true> {  // one dword (scale | bias << 16) per group
-    uint32_t v[NG];
-};
-template <int NG>
-struct Meta<NG, false> {  // NG scales and NG biases, two per dword
-    uint32_t s[(NG + 1) / 2], b[(NG + 1) / 2];
+// (Vector types, not arrays: an array member of the ring's slots can keep the
+// whole ring out of registers.)
+template <>
+struct Meta<1, true> {  // one dword (scale | bias << 16) per group
+    uint32_t v;
 };
 template <>
+struct Meta<2, true> {
+    u32x2 v;
+};
+template <>
+struct Meta<4, true> {
+    u32x4 v;
+};
+template <int NG>
+__device__ __forceinline__ uint32_t mword(const Meta<NG, true>& m, int gi) {
+    if constexpr (NG == 1) return m.v;
+    else return m.v[gi];
+}
+template <>
 struct Meta<1, false> {  // one scale, one bias: kept 16-bit until use
-    uint16_t s[1], b[1];
+    uint16_t s, b;
+};
+template <>
+struct Meta<2, false> {  // two scales, two biases, one dword each
+    uint32_t s, b;
+};
+template <>
+struct Meta<4, false> {
+    u32x2 s, b;
 };
 
 template <int NG, bool SB>
-struct Slot {
-    u32x4 w;
-    Meta<NG, SB> m;
-};
-
-template <int NG, bool SB>
-__device__ __forceinline__ void load_meta(Meta<NG, SB>& m, const uint16_t* __restrict__ S,
-                                          const uint16_t* __restrict__ B, size_t gi) {
+__device__ __forceinline__ void load_meta(Meta<NG, SB>& m, rsrc_t rs, rsrc_t rb, uint32_t vo,
+                                          uint32_t so) {
     if constexpr (SB) {
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(S) + gi;
-        if constexpr (NG == 1) {
-            m.v[0] = *p;
-        } else if constexpr (NG == 2) {
-            const u32x2 t = *reinterpret_cast<const u32x2*>(p);
-            m.v[0] = t.x;
-            m.v[1] = t.y;
-        } else {
-            const u32x4 t = *reinterpret_cast<const u32x4*>(p);
-            m.v[0] = t.x;
-            m.v[1] = t.y;
-            m.v[2] = t.z;
-            m.v[3] = t.w;
-        }
+        if constexpr (NG == 1) m.v = __builtin_amdgcn_raw_buffer_load_b32(rs, vo, so, 0);
+        else if constexpr (NG == 2) m.v = __builtin_amdgcn_raw_buffer_load_b64(rs, vo, so, 0);
+        else m.v = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, so, 0);
+    } else if constexpr (NG == 1) {
+        m.s = __builtin_amdgcn_raw_buffer_load_b16(rs, vo, so, 0);
+        m.b = __builtin_amdgcn_raw_buffer_load_b16(rb, vo, so, 0);
+    } else if constexpr (NG == 2) {
+        m.s = __builtin_amdgcn_raw_buffer_load_b32(rs, vo, so, 0);
+        m.b = __builtin_amdgcn_raw_buffer_load_b32(rb, vo, so, 0);
     } else {
-        if constexpr (NG == 1) {
-            m.s[0] = S[gi];
-            m.b[0] = B[gi];
-        } else if constexpr (NG == 2) {
-            m.s[0] = *reinterpret_cast<const uint32_t*>(S + gi);
-            m.b[0] = *reinterpret_cast<const uint32_t*>(B + gi);
-        } else {
-            const u32x2 s2 = *reinterpret_cast<const u32x2*>(S + gi);
-            const u32x2 b2 = *reinterpret_cast<const u32x2*>(B + gi);
-            m.s[0] = s2.x;
-            m.s[1] = s2.y;
-            m.b[0] = b2.x;
-            m.b[1] = b2.y;
-        }
+        m.s = __builtin_amdgcn_raw_buffer_load_b64(rs, vo, so, 0);
+        m.b = __builtin_amdgcn_raw_buffer_load_b64(rb, vo, so, 0);
     }
 }
 
+// Low 16 bits of `raw` as a float (fp16 or bf16 bits).
+template <bool BF>
+__device__ __forceinline__ float lo16f(uint32_t raw) {
+    if constexpr (BF) return __builtin_bit_cast(float, raw << 16);
+    else return (float)__builtin_bit_cast(_Float16, (uint16_t)raw);
+}
+
+// Scale of group gi for this lane's row.
 template <int NG, bool SB, bool BF>
-__device__ __forceinline__ float2 meta_sb(const Meta<NG, SB>& m, int gg) {
-    uint32_t sv, bv;
+__device__ __forceinline__ float sval(const Meta<NG, SB>& m, int gi) {
+    uint32_t raw;
+    if constexpr (SB) raw = mword<NG>(m, gi);
+    else if constexpr (NG == 1) raw = m.s;
+    else if constexpr (NG == 2) raw = gi ? m.s >> 16 : m.s;
+    else raw = (gi & 1) ? m.s[gi >> 1] >> 16 : m.s[gi >> 1];
+    return lo16f<BF>(raw);
+}
+
+// B operand of the correction MFMA of group pair p for lane group kg:
+// kg = 0: bias of group 2p, 1: scale of 2p, 2: bias of 2p+1, 3: scale of 2p+1
+// (zero where the group does not exist). shs = 16 for biases, 0 for scales
+// (interleaved dwords); hsel = 16 * (kg >> 1) (separate arrays).
+template <int NG, bool SB, bool BF>
+__device__ __forceinline__ float bcorr(const Meta<NG, SB>& m, int p, bool hi_grp, bool want_s,
+                                       uint32_t shs, uint32_t hsel) {
+    uint32_t raw;
     if constexpr (SB) {
-        sv = m.v[gg] & 0xFFFFu;
-        bv = m.v[gg] >> 16;
+        uint32_t d;
+        if constexpr (NG == 1) d = hi_grp ? 0u : m.v;
+        else d = hi_grp ? m.v[2 * p + 1] : m.v[2 * p];
+        raw = d >> shs;
+    } else if constexpr (NG == 1) {
+        const uint32_t d = want_s ? (uint32_t)m.s : (uint32_t)m.b;
+        raw = hi_grp ? 0u : d;
+    } else if constexpr (NG == 2) {
+        raw = (want_s ? m.s : m.b) >> hsel;
     } else {
-        const int h = (gg & 1) * 16;
-        sv = (m.s[gg >> 1] >> h) & 0xFFFFu;
-        bv = (m.b[gg >> 1] >> h) & 0xFFFFu;
+        raw = (want_s ? m.s[p] : m.b[p]) >> hsel;
     }
-    if constexpr (BF) return make_float2(bf2f((uint16_t)sv), bf2f((uint16_t)bv));
-    else return make_float2(h2f((uint16_t)sv), h2f((uint16_t)bv));
+    return lo16f<BF>(raw);
 }
 
 // Word (of the span's 16) that register j of lane group g holds after regroup.
@@ -180,8 +228,15 @@ __device__ __forceinline__ f16x8 dq(uint32_t w, const DequantConsts& k) {
     return __builtin_bit_cast(f16x8, t);
 }
 
-__device__ __forceinline__ f32x4 mfma(u32x4 a, f16x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), b, c, 0, 0, 0);
+// x pairs (x0,x1)(x2,x3)(x4,x5)(x6,x7) -> dequant order (x0,x4)(x1,x5)(x2,x6)(x3,x7).
+__device__ __forceinline__ f16x8 xperm(u32x4 v) {
+    const u32x4 p{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                  __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
+    return __builtin_bit_cast(f16x8, p);
+}
+
+__device__ __forceinline__ f32x4 mma16(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 // Position of a wave in its (round, span) sequence.
@@ -195,82 +250,80 @@ struct Cursor {
     }
 };
 
-// LDS: xp [ntok][K/8] u32x4 | xk [ntok][K/G] float2 | part [2][waves][RMAX][64] f32
-__host__ __device__ inline size_t lds_xp(uint32_t ntok, uint32_t K) { return (size_t)ntok * K * 2; }
-__host__ __device__ inline size_t lds_xk(uint32_t ntok, uint32_t K, uint32_t G) {
-    return (size_t)ntok * (K / G) * 8;
-}
-__host__ __device__ inline size_t lds_part(uint32_t waves, uint32_t rmax) {
-    return (size_t)2 * waves * rmax * 64 * 4;
-}
+template <int GM, bool SB, int T>
+struct Slot {
+    u32x4 w[T];
+    Meta<128 / GM, SB> m[T];
+    u32x4 x[4];
+};
 
-template <int GM, bool SB, bool BF, int RMAX, int D>
-__global__ __launch_bounds__(1024) void int4_mfma(Args A) {
-    constexpr int NG = 128 / GM;  // quant groups per span
-    constexpr int WPG = GM / 8;   // words per group
-    using SlotT = Slot<NG, SB>;
+template <int GM, bool SB, bool BF, int T, int D, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
+    constexpr int NG = 128 / GM;       // quant groups per span
+    constexpr int NP = (NG + 1) / 2;   // group pairs (correction MFMAs) per span
+    constexpr int PER = 4 / NG;        // MFMAs per group
+    constexpr uint32_t MB = SB ? 4 : 2;  // meta bytes per group (per array)
+    using SlotT = Slot<GM, SB, T>;
 
     extern __shared__ __align__(16) unsigned char smem[];
-    const uint32_t K = A.K, nw = K >> 3, ngr = K / GM;
-    u32x4* xp = reinterpret_cast<u32x4*>(smem);
-    float2* xk = reinterpret_cast<float2*>(smem + lds_xp(A.ntok, K));
-    float* part = reinterpret_cast<float*>(smem + lds_xp(A.ntok, K) + lds_xk(A.ntok, K, GM));
+    float* part = reinterpret_cast<float*>(smem);
 
+    const uint32_t K = A.K, M = A.M;
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
-    const int lane = tid & 63;
-    const uint32_t wave = tid >> 6;
+    // the wave index is uniform; say so, or every buffer load whose scalar
+    // offset derives from it becomes a waterfall loop
+    const uint32_t lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t p = wave % A.P, q = wave / A.P;
-    const uint32_t lrow = lane & 15, lg = lane >> 4;
-    const uint32_t tile0 = blockIdx.x * A.tiles_wg;
-    const uint32_t last_tile = A.ntiles - 1, last_row = A.M - 1;
+    const uint32_t n = lane & 15, kg = lane >> 4;
+    const uint32_t g0 = blockIdx.x * A.groups_wg;
 
-    // ---- 1. first x staging loads (before any weight load: vmcnt is in order)
-    const uint32_t xtotal = A.ntok * nw;
-    const u32x4* X4 = reinterpret_cast<const u32x4*>(A.X);
-    constexpr int kXr = 4;  // staging rounds per batch of loads
-    u32x4 sv[kXr];
-    auto x_load = [&](uint32_t w0) {
+    const rsrc_t rW = make_rsrc(A.W, M * (K / 2));
+    const rsrc_t rS = make_rsrc(A.S, M * A.gpr * MB);
+    const rsrc_t rB = make_rsrc(SB ? A.S : A.B, M * A.gpr * MB);
+    const rsrc_t rX = make_rsrc(A.X, A.ntok * K * 2);
+
+    // lane-constant parts of the x addresses (token n, clamped into the batch)
+    uint32_t xvo[4];
+    {
+        const uint32_t t = n < A.ntok ? n : A.ntok - 1;
 #pragma unroll
-        for (int r = 0; r < kXr; ++r) {
-            const uint32_t w = w0 + r * nthr + tid;
-            sv[r] = X4[w < xtotal ? w : xtotal - 1];
+        for (int j = 0; j < 4; ++j) xvo[j] = t * K * 2 + xword<GM>(j, kg) * 16;
+    }
+
+    // lane-constant parts of the weight / meta addresses of the current issue round
+    uint32_t wvo[T], mvo[T];
+    uint32_t cur_rg = 0xFFFFFFFFu;
+    auto set_rows = [&](uint32_t rg) {
+        cur_rg = rg;
+#pragma unroll
+        for (int i = 0; i < T; ++i) {
+            uint32_t row = rg * (16 * T) + 16 * i + n;
+            row = row < M ? row : M - 1;
+            wvo[i] = row * (K / 2) + kg * 16;
+            mvo[i] = row * A.gpr * MB;
         }
     };
-    auto x_store = [&](uint32_t w0) {
-#pragma unroll
-        for (int r = 0; r < kXr; ++r) {
-            const uint32_t w = w0 + r * nthr + tid;
-            float s, c;
-            word_consts(sv[r], s, c);
-#pragma unroll
-            for (int o = 1; o < WPG; o <<= 1) {
-                s += __shfl_xor(s, o);
-                c += __shfl_xor(c, o);
-            }
-            if (w < xtotal) {
-                xp[w] = pair_perm(sv[r]);
-                if (w % WPG == 0) xk[w / WPG] = make_float2(s, c);
-            }
-        }
-    };
-    x_load(0);
-    // The scheduler may not interleave these loads: the loop's waits are
-    // derived from the order they are issued in (also on entry to the loop).
-    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- 2. prime the ring
+    // ---- prime the ring (one straight sequence of loads)
     SlotT ring[D];
     auto issue = [&](SlotT& e, Cursor c) {
         if (c.round >= A.rounds) {  // padding step: re-read the last real one
             c.round = A.rounds - 1;
             c.j = A.J - 1;
         }
-        const uint32_t tile = min(tile0 + c.round * A.Q + q, last_tile);
-        const uint32_t row = min(tile * kTile + lrow, last_row);
-        const uint32_t span = p * A.J + c.j;
-        const u32x4* wp = reinterpret_cast<const u32x4*>(A.W + (size_t)row * nw + span * 16) + lg;
-        e.w = ldg_nt(wp);
-        load_meta<NG, SB>(e.m, A.S, A.B, (size_t)row * A.gpr + span * NG);
+        uint32_t rg = g0 + c.round * A.Q + q;
+        rg = __builtin_amdgcn_readfirstlane(rg < A.ngroups ? rg : A.ngroups - 1);
+        if (rg != cur_rg) set_rows(rg);
+        // uniform by construction; readfirstlane keeps it in an SGPR (a scalar
+        // offset the compiler thinks divergent becomes a waterfall loop)
+        const uint32_t span = __builtin_amdgcn_readfirstlane(p * A.J + c.j);
+#pragma unroll
+        for (int i = 0; i < T; ++i) {
+            e.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rW, wvo[i], span * 64, kNT);
+            load_meta<NG, SB>(e.m[i], rS, rB, mvo[i], span * NG * MB);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rX, xvo[j], span * 256, 0);
     };
     Cursor ci{0, 0};
 #pragma unroll
@@ -280,97 +333,106 @@ __global__ __launch_bounds__(1024) void int4_mfma(Args A) {
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- 3. finish the x staging
-    x_store(0);
-    for (uint32_t w0 = kXr * nthr; w0 < xtotal; w0 += kXr * nthr) {
-        x_load(w0);
-        x_store(w0);
-    }
-    __syncthreads();
-
-    // ---- 4. per-lane constants
+    // ---- per-lane constants
     const DequantConsts kc;
-    const bool has_tok = lrow < A.ntok;
-    const u32x4* xrow = xp + (size_t)(has_tok ? lrow : 0) * nw;
-    uint32_t xo[4];
+    // constant A operands of the sums MFMA, one per group of the span
+    f16x8 ac[NG];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xo[j] = xword<GM>(j, lg);
-    const float2* xkr[RMAX];
-#pragma unroll
-    for (int r = 0; r < RMAX; ++r) {
-        const uint32_t t = min(4 * lg + r, A.ntok - 1);
-        xkr[r] = xk + (size_t)t * ngr;
+    for (int gi = 0; gi < NG; ++gi) {
+        const uint32_t rs = 8 * (gi & 1) + (gi >> 1), rc = rs + 4;
+        const u32x4 ones{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
+        const u32x4 negm{0xE400E400u, 0xD400D400u, 0xE400E400u, 0xD400D400u};
+        const u32x4 zero{0u, 0u, 0u, 0u};
+        ac[gi] = __builtin_bit_cast(f16x8, n == rs ? ones : n == rc ? negm : zero);
     }
-    u32x4 xa[4];
+    const bool hi_grp = kg >= 2, want_s = (kg & 1) != 0;
+    const uint32_t shs = want_s ? 0u : 16u, hsel = hi_grp ? 16u : 0u;
+    f32x4 acc[T];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xa[j] = u32x4{0, 0, 0, 0};
-    float acc[RMAX];
-#pragma unroll
-    for (int r = 0; r < RMAX; ++r) acc[r] = 0.0f;
+    for (int i = 0; i < T; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // ---- 5. one step: compute a slot, close the unit at the end of a part
+    // ---- close a round: sum the P parts (LDS, fixed order) and store y
+    auto store = [&](uint32_t row, uint32_t t, float v) {
+        if (t < A.ntok && row < M) {
+            const size_t o = (size_t)t * M + row;
+            if (A.y_f32) reinterpret_cast<float*>(A.Y)[o] = v;
+            else reinterpret_cast<uint16_t*>(A.Y)[o] = f2h(v);
+        }
+    };
     auto finish = [&](uint32_t round) {
-        float* pw = part + (size_t)((round & 1) * (A.P * A.Q) + wave) * RMAX * 64;
+        const uint32_t rgw = g0 + round * A.Q;  // first row group of this round in the workgroup
+        if (A.P == 1) {
+            const uint32_t rg = rgw + q;
+            if (rg < A.ngroups) {
 #pragma unroll
-        for (int r = 0; r < RMAX; ++r) {
-            pw[r * 64 + lane] = acc[r];
-            acc[r] = 0.0f;
-        }
-        __syncthreads();
-        const uint32_t per_tile = kTile * A.ntok, nout = A.Q * per_tile;
-        const float* pr = part + (size_t)(round & 1) * (A.P * A.Q) * RMAX * 64;
-        for (uint32_t i = tid; i < nout; i += nthr) {
-            const uint32_t qq = i / per_tile, rem = i - qq * per_tile;
-            const uint32_t t = rem >> 4, n = rem & 15;
-            const uint32_t ls = 16 * (t >> 2) + n, r = t & 3;
-            float v = 0.0f;
-            for (uint32_t pp = 0; pp < A.P; ++pp)
-                v += pr[(size_t)((qq * A.P + pp) * RMAX + r) * 64 + ls];
-            const uint32_t tl = round * A.Q + qq, tile = tile0 + tl;
-            const uint32_t row = tile * kTile + n;
-            if (tl < A.tiles_wg && tile < A.ntiles && row < A.M) {
-                const size_t o = (size_t)t * A.M + row;
-                if (A.y_f32) reinterpret_cast<float*>(A.Y)[o] = v;
-                else reinterpret_cast<uint16_t*>(A.Y)[o] = f2h(v);
+                for (int i = 0; i < T; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) store(rg * (16 * T) + 16 * i + n, 4 * kg + r, acc[i][r]);
+            }
+        } else {
+            float* pw = part + ((size_t)((A.rounds > 1 ? (round & 1) : 0) * (A.P * A.Q) + wave) * T) * 256;
+#pragma unroll
+            for (int i = 0; i < T; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) pw[(i * 4 + r) * 64 + lane] = acc[i][r];
+            __syncthreads();
+            const float* pr = part + (size_t)((A.rounds > 1 ? (round & 1) : 0) * (A.P * A.Q)) * T * 256;
+            const uint32_t per_grp = T * 16 * A.ntok, nout = A.Q * per_grp;
+            for (uint32_t o = tid; o < nout; o += nthr) {
+                const uint32_t qq = o / per_grp, rem = o - qq * per_grp;
+                const uint32_t i = rem / (16 * A.ntok), rem2 = rem - i * 16 * A.ntok;
+                const uint32_t t = rem2 >> 4, nn = rem2 & 15;
+                const uint32_t ls = 16 * (t >> 2) + nn, r = t & 3;
+                float v = 0.0f;
+                for (uint32_t pp = 0; pp < A.P; ++pp) v += pr[((size_t)(qq * A.P + pp) * T * 4 + i * 4 + r) * 64 + ls];
+                const uint32_t rg = rgw + qq;
+                if (rg < A.ngroups) store(rg * (16 * T) + 16 * i + nn, t, v);
             }
         }
-    };
-    auto step = [&](const SlotT& e, Cursor c, uint32_t n) {
-        const uint32_t span = p * A.J + c.j;
-        if (has_tok) {
-            const u32x4* xs = xrow + span * 16;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xa[j] = xs[xo[j]];
-        }
-        uint32_t w[4] = {e.w.x, e.w.y, e.w.z, e.w.w};
-        regroup<GM>(w);
-        f32x4 dacc[NG];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            constexpr int per = 4 / NG;
-            const int gg = j / per;
-            const f32x4 cin = (j % per == 0) ? f32x4{0, 0, 0, 0} : dacc[gg];
-            dacc[gg] = mfma(xa[j], dq(w[j], kc), cin);
-        }
-#pragma unroll
-        for (int gg = 0; gg < NG; ++gg) {
-            const float2 sb = meta_sb<NG, SB, BF>(e.m, gg);
-#pragma unroll
-            for (int r = 0; r < RMAX; ++r) {
-                const float2 k2 = xkr[r][span * NG + gg];
-                acc[r] = fmaf(sb.x, dacc[gg][r] - k2.y, fmaf(sb.y, k2.x, acc[r]));
-            }
-        }
-        if (n < A.nreal && c.j == A.J - 1) finish(c.round);
+        for (int i = 0; i < T; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     };
 
-    // ---- 6. main loop (loads D steps ahead), then the last D steps
+    // ---- one step: x-only sums, then per tile the group MFMAs and epilogue
+    auto step = [&](const SlotT& e, Cursor c, uint32_t nstep) {
+        f16x8 xa[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xa[j] = xperm(e.x[j]);
+        f32x4 sums{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sums = mma16(ac[j / PER], xa[j], sums);
+#pragma unroll
+        for (int i = 0; i < T; ++i) {
+            uint32_t w[4] = {e.w[i].x, e.w[i].y, e.w[i].z, e.w[i].w};
+            regroup<GM>(w);
+            f32x4 dg[NG];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int gi = j / PER;
+                const f32x4 cin = (j % PER == 0) ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : dg[gi];
+                dg[gi] = mma16(xa[j], dq(w[j], kc), cin);
+            }
+#pragma unroll
+            for (int gi = 0; gi < NG; ++gi) {
+                const float s = sval<NG, SB, BF>(e.m[i], gi);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(s, dg[gi][r], acc[i][r]);
+            }
+#pragma unroll
+            for (int pp = 0; pp < NP; ++pp)
+                acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                    sums[pp], bcorr<NG, SB, BF>(e.m[i], pp, hi_grp, want_s, shs, hsel), acc[i], 0, 0, 0);
+        }
+        if (nstep < A.nreal && c.j == A.J - 1) finish(c.round);
+    };
+
+    // ---- main loop (loads D steps ahead), then the last D steps
     Cursor cc{0, 0};
-    uint32_t n = 0;
-    for (; n + D < A.nsteps; n += D) {
+    uint32_t ns = 0;
+    for (; ns + D < A.nsteps; ns += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            step(ring[d], cc, n + d);
+            step(ring[d], cc, ns + d);
             cc.advance(A.J);
             issue(ring[d], ci);
             ci.advance(A.J);
@@ -378,45 +440,37 @@ __global__ __launch_bounds__(1024) void int4_mfma(Args A) {
     }
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-        step(ring[d], cc, n + d);
+        step(ring[d], cc, ns + d);
         cc.advance(A.J);
     }
 }
 
-template <int GM, bool SB, bool BF, int RMAX, int D>
+template <int GM, bool SB, bool BF, int T, int D, int WAVES>
 hipError_t go(const Args& a, const Plan& pl, hipStream_t s) {
-    auto kern = int4_mfma<GM, SB, BF, RMAX, D>;
+    auto kern = int4_mfma<GM, SB, BF, T, D, WAVES>;
     if (pl.lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)pl.lds);
         if (e != hipSuccess) return e;
     }
-    kern<<<pl.nwg, pl.P * pl.Q * 64, pl.lds, s>>>(a);
+    kern<<<pl.nwg, pl.waves * 64, pl.lds, s>>>(a);
     return hipGetLastError();
 }
 
-template <int GM, bool SB, bool BF, int RMAX>
-hipError_t go_d(const Args& a, const Plan& pl, hipStream_t s) {
-    switch (pl.D) {
-        case 2: return go<GM, SB, BF, RMAX, 2>(a, pl, s);
-        case 4: return go<GM, SB, BF, RMAX, 4>(a, pl, s);
-        case 8: return go<GM, SB, BF, RMAX, 8>(a, pl, s);
-        default: return hipErrorInvalidValue;
-    }
+template <int GM, bool SB, bool BF>
+hipError_t go_td(const Args& a, const Plan& pl, hipStream_t s) {
+    if (pl.T == 4 && pl.D == 2) return go<GM, SB, BF, 4, 2, max_waves(GM, 4, 2)>(a, pl, s);
+    if (pl.T == 2 && pl.D == 2) return go<GM, SB, BF, 2, 2, max_waves(GM, 2, 2)>(a, pl, s);
+    if (pl.T == 1 && pl.D == 2) return go<GM, SB, BF, 1, 2, max_waves(GM, 1, 2)>(a, pl, s);
+    if (pl.T == 1 && pl.D == 3) return go<GM, SB, BF, 1, 3, max_waves(GM, 1, 3)>(a, pl, s);
+    return hipErrorInvalidValue;
 }
 
 template <int GM>
 hipError_t dispatch(const Args& a, const Plan& pl, bool sb, bool bf, hipStream_t s) {
-#define KQ_R(SBV, BFV)                                                             \
-    return pl.rmax == 1 ? go_d<GM, SBV, BFV, 1>(a, pl, s) : go_d<GM, SBV, BFV, 4>(a, pl, s)
-    if (sb) {
-        if (bf) KQ_R(true, true);
-        KQ_R(true, false);
-    }
-    if (bf) KQ_R(false, true);
-    KQ_R(false, false);
-#undef KQ_R
+    if (sb) return bf ? go_td<GM, true, true>(a, pl, s) : go_td<GM, true, false>(a, pl, s);
+    return bf ? go_td<GM, false, true>(a, pl, s) : go_td<GM, false, false>(a, pl, s);
 }
 
 }  // namespace mfma

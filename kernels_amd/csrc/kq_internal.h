@@ -10,8 +10,8 @@
 namespace kq {
 
 struct Int4Cfg {
-    int rows;    // rows per wave (VALU) / row tiles of 32 per wave (MFMA)
-    int unroll;  // 64-chunk steps whose loads are issued before any is used
+    int rows;    // VALU: rows per wave item; MFMA: K parts per workgroup
+    int unroll;  // VALU: ring depth; MFMA: ring depth D, or 10 * tiles per wave + D
 };
 
 // Default launch shape for a problem (tuning table).
@@ -26,9 +26,9 @@ bool int4_valu_supported(uint32_t K, uint32_t batch, Int4Cfg cfg);
 hipError_t launch_int4_mfma(const uint32_t* W, const uint16_t* S, const uint16_t* B, int meta_kind,
                             bool interleaved, const uint16_t* X, void* Y, bool y_f32, uint32_t M,
                             uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg, hipStream_t s);
-bool int4_mfma_supported(uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg);
+bool int4_mfma_supported(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg);
 Int4Cfg int4_mfma_default(uint32_t M, uint32_t K, uint32_t batch);
-// Tokens one matrix-core pass stages in LDS (0: the shape is not supported).
+// Tokens one matrix-core pass takes (all of them; 0: the shape is not supported).
 uint32_t int4_mfma_tokens_per_pass(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg);
 
 hipError_t launch_xsum32(const uint16_t* X, float* xs, uint32_t K, uint32_t batch, hipStream_t s);

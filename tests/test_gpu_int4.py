@@ -121,90 +121,27 @@ def test_forced_launch_shapes_agree(gpu, K, parts, depth, M, batch):
     check(got, ref_int4(p), f"P={parts} D={depth} K={K} M={M} b={batch}")
 
 
-@pytest.mark.parametrize("parts,depth", [(3, 4), (1, 3)])
-def test_forced_launch_shape_unsupported(gpu, parts, depth):
-    p = gen.int4_problem(64, 8192, 64, seed=1)
-    with pytest.raises(kq.KQError) as e:
-        run_int4(p, gpu, path=kq.PATH_VALU, rows=parts, unroll=depth)  # 3 does not divide 4 steps
-    assert e.value.status == kq.KQ_EUNSUPPORTED
+# (K parts P, 10 * tiles per wave T + ring depth D)
+MFMA_PLANS = [(16, 12), (16, 13), (8, 22), (2, 22), (4, 42), (8, 42), (1, 42), (1, 13)]
 
 
-def test_deterministic(gpu):
-    p = gen.int4_problem(4096, 4096, 64, seed=5)
-    a = run_int4(p, gpu)
-    b = run_int4(p, gpu)
-    assert np.array_equal(a, b)
-
-
-def test_xsum32_bit_exact(gpu):
-    rng = np.random.default_rng(2)
-    K, batch = 14336, 3
-    X = gen.f16_bits(rng.normal(0, 1, (batch, K)))
-    xs = torch.empty((batch, K // 32), dtype=torch.float32, device=gpu)
-    kq.xsum32(dev(X, gpu), xs, K, batch)
-    torch.cuda.synchronize()
-    assert np.array_equal(xs.cpu().numpy(), oracle.xsum32(X, K))
-
-
-def test_stream_read_runs(gpu):
-    n = 64 << 20
-    src = torch.zeros(n // 4, dtype=torch.int32, device=gpu)
-    sink = torch.zeros(4, dtype=torch.int32, device=gpu)
-    kq.stream_read(src, n, sink)
-    torch.cuda.synchronize()
-    assert sink.cpu().tolist() == [0, 0, 0, 0]  # fold of zeros is not all ones
-
-
-@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 8, 9, 16])
-@pytest.mark.parametrize("M,K,G", [(4096, 4096, 64), (1031, 14336, 64), (777, 2944, 64),
-                                   (300, 8192, 128), (64, 28672, 64), (33, 1152, 128),
-                                   (513, 4096, 32), (100, 1024, 32)])
-def test_mfma_path(gpu, M, K, G, batch):
-    """Matrix-core path: 16-row tiles, K split over the waves of a
-    workgroup and summed in LDS; G = 32 / 64 / 128 regroup the loaded words
-    with 4 / 2 / 0 lane swaps; batches past one LDS pass re-run over token
-    groups."""
-    p = gen.int4_problem(M, K, G, batch=batch, seed=M + K + G + batch)
-    check(run_int4(p, gpu, path=kq.PATH_MFMA), ref_int4(p), f"mfma M={M} K={K} G={G} b={batch}")
-
-
-@pytest.mark.parametrize("layout", ["sb", "split"])
-def test_mfma_layouts_bf16_fp32out(gpu, layout):
-    p = gen.int4_problem(515, 4096, 64, batch=2, seed=21, dist="ref")
-    check(run_int4(p, gpu, layout=layout, path=kq.PATH_MFMA, y_dtype=torch.float32),
-          ref_int4(p, layout), f"mfma {layout}")
-    rng = np.random.default_rng(5)
-    S = gen.bf16_bits(np.abs(rng.normal(0, 0.02, (515, 64))))
-    B = gen.bf16_bits(rng.normal(0, 0.02, (515, 64)))
-    ref = oracle.int4_gemv(p["W"], S, B, p["X"], 515, 4096, 64, 0, oracle.BF16)
-    check(run_int4(p, gpu, layout="split", sb_dtype=kq.BF16, S=S, B=B, path=kq.PATH_MFMA), ref,
-          "mfma bf16")
-
-
-@pytest.mark.parametrize("K,G", [(1056, 32), (2880, 64)])
-def test_mfma_unsupported_falls_back(gpu, K, G):
-    """The matrix-core path needs K % 128 == 0; forcing it otherwise is
-    refused, and the automatic choice uses the vector path."""
-    p = gen.int4_problem(64, K, G, batch=8, seed=2)
-    with pytest.raises(kq.KQError) as e:
-        run_int4(p, gpu, path=kq.PATH_MFMA)
-    assert e.value.status == kq.KQ_EUNSUPPORTED
-    check(run_int4(p, gpu), ref_int4(p), f"auto path K={K} G={G}")
-
-
-@pytest.mark.parametrize("parts,depth", [(16, 2), (16, 8), (8, 4), (4, 2), (2, 8), (1, 4)])
-@pytest.mark.parametrize("M,batch", [(1000, 1), (257, 5)])
-def test_mfma_forced_plans_agree(gpu, parts, depth, M, batch):
-    """Every (K parts, ring depth) plan of the matrix-core path gives the
-    oracle's result: padding steps, idle tile lanes and several rounds per
-    workgroup included (K = 4096: 32 spans)."""
-    p = gen.int4_problem(M, 4096, 64, batch=batch, seed=parts * 10 + depth)
-    got = run_int4(p, gpu, path=kq.PATH_MFMA, rows=parts, unroll=depth)
-    check(got, ref_int4(p), f"mfma P={parts} D={depth} M={M} b={batch}")
+@pytest.mark.parametrize("parts,unroll", MFMA_PLANS)
+@pytest.mark.parametrize("M,batch", [(1000, 1), (257, 5), (9600, 3)])
+def test_mfma_forced_plans_agree(gpu, parts, unroll, M, batch):
+    """Every (K parts, tiles per wave, ring depth) plan of the matrix-core
+    path gives the oracle's result: padding steps, clamped rows, idle lanes
+    and several rounds per workgroup (M = 9600: 600 tiles) included
+    (K = 4096: 32 spans)."""
+    p = gen.int4_problem(M, 4096, 64, batch=batch, seed=parts * 100 + unroll + M)
+    got = run_int4(p, gpu, path=kq.PATH_MFMA, rows=parts, unroll=unroll)
+    check(got, ref_int4(p), f"mfma P={parts} T,D={unroll} M={M} b={batch}")
 
 
 def test_mfma_forced_plan_unsupported(gpu):
     p = gen.int4_problem(64, 4096, 64, seed=3)
     with pytest.raises(kq.KQError) as e:
-        run_int4(p, gpu, path=kq.PATH_MFMA, rows=3, unroll=4)  # 3 does not divide 32 spans
+        run_int4(p, gpu, path=kq.PATH_MFMA, rows=3, unroll=12)  # 3 does not divide 32 spans
+    assert e.value.status == kq.KQ_EUNSUPPORTED
+    with pytest.raises(kq.KQError) as e:
+        run_int4(p, gpu, path=kq.PATH_MFMA, rows=16, unroll=42)  # T = 4 has 8 waves
     assert e.value.status == kq.KQ_EUNSUPPORTED
