@@ -120,6 +120,21 @@ kq_status check_ws(const kq_moe_desc* d, uint32_t batch, const void* ws, size_t 
 
 }  // namespace
 
+namespace kq {
+uint32_t cu_count() {
+    static int n = 0;
+    if (n <= 0) {
+        int dev = 0, v = 0;
+        n = hipGetDevice(&dev) == hipSuccess &&
+                    hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+                    v > 0
+                ? v
+                : 256;
+    }
+    return (uint32_t)n;
+}
+}  // namespace kq
+
 extern "C" {
 
 const char* kq_status_str(kq_status s) {

@@ -151,6 +151,19 @@ __device__ __forceinline__ float qdot8(uint32_t w, u32x4 p, float acc) {
     return acc;
 }
 
+// Raw buffer descriptor (stride 0; word 3 = the gfx9 default data format).
+// Buffer loads address with a VGPR offset plus an SGPR offset; `bytes` is the
+// range the hardware checks (< 2 GiB here).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+// Cache policies of buffer loads / stores: non-temporal (streamed weights);
+// device-coherent (sc1: what agent-scope relaxed atomics use -- data shared
+// between workgroups of one launch without an L2 write-back).
+constexpr int kNT = 2;
+constexpr int kSC1 = 16;
+
 template <typename T>
 __device__ __forceinline__ T ldg_nt(const T* p) {
     return __builtin_nontemporal_load(p);

@@ -287,20 +287,6 @@ __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
     }
 }
 
-int g_num_cu = 0;
-
-uint32_t num_cu() {
-    if (g_num_cu <= 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-            n > 0)
-            g_num_cu = n;
-        else
-            g_num_cu = 256;
-    }
-    return (uint32_t)g_num_cu;
-}
 
 constexpr size_t kLdsMax = 160 * 1024;
 constexpr uint32_t kMaxNB = 2;  // tokens per pass of the vector path
@@ -320,7 +306,7 @@ uint32_t log2u(uint32_t v) {
 // Among (R, P) with equal per-CU work, one x read shared by 2 rows and fewer
 // K parts (no LDS reduction) win.
 bool make_vplan(uint32_t M, uint32_t K, uint32_t ntok, Int4Cfg cfg, VPlan& out) {
-    const uint32_t nch = K >> 5, nstep = (nch + 63) / 64, nchp = nstep * 64, cu = num_cu();
+    const uint32_t nch = K >> 5, nstep = (nch + 63) / 64, nchp = nstep * 64, cu = cu_count();
     if (cfg.unroll != 0 && cfg.unroll != 2 && cfg.unroll != 4 && cfg.unroll != 8) return false;
     bool found = false;
     double best = 0.0;

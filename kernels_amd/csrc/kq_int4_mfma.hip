@@ -16,25 +16,12 @@ namespace kq {
 
 namespace {
 
-int g_ncu = 0;
-uint32_t ncu() {
-    if (g_ncu <= 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-            n > 0)
-            g_ncu = n;
-        else
-            g_ncu = 256;
-    }
-    return (uint32_t)g_ncu;
-}
 
 constexpr size_t kLdsMax = 160 * 1024;
 
 bool make_plan(uint32_t M, uint32_t K, uint32_t G, uint32_t ntok, Int4Cfg cfg, mfma::Plan& out) {
     (void)ntok;
-    const uint32_t nspan = K / 128, ntiles = (M + mfma::kTile - 1) / mfma::kTile, cu = ncu();
+    const uint32_t nspan = K / 128, ntiles = (M + mfma::kTile - 1) / mfma::kTile, cu = cu_count();
     // cfg.unroll: 0 = automatic, D (2, 3) or 10 * T + D; cfg.rows: K parts P (0 = automatic)
     uint32_t fT = 0, fD = 0;
     if (cfg.unroll >= 10) {

@@ -90,12 +90,6 @@ __host__ __device__ inline size_t lds_part(uint32_t waves, uint32_t T, uint32_t 
     return P > 1 ? (size_t)(rounds > 1 ? 2 : 1) * waves * T * 4 * 64 * 4 : 0;
 }
 
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-// Raw buffer descriptor (stride 0; word 3 = gfx9 default data format).
-__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-constexpr int kNT = 2;  // cache policy of streamed weights: non-temporal
 
 // Scale/bias registers of one span (NG groups), converted at use.
 template <int NG, bool SB>

@@ -14,6 +14,9 @@ struct Int4Cfg {
     int unroll;  // VALU: ring depth; MFMA: ring depth D, or 10 * tiles per wave + D
 };
 
+// Compute units of the current device (queried once; 256 if the query fails).
+uint32_t cu_count();
+
 // Default launch shape for a problem (tuning table).
 Int4Cfg int4_valu_default(uint32_t M, uint32_t K, uint32_t batch);
 size_t int4_valu_lds_bytes(uint32_t K, uint32_t batch);

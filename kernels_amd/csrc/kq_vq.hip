@@ -271,25 +271,12 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
     }
 }
 
-int g_vq_ncu = 0;
-uint32_t vq_ncu() {
-    if (g_vq_ncu <= 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-            n > 0)
-            g_vq_ncu = n;
-        else
-            g_vq_ncu = 256;
-    }
-    return (uint32_t)g_vq_ncu;
-}
 
 // Plan as for the int4 vector path (kq_int4.hip, make_vplan): spread row
 // groups over every CU, no idle lanes, 2-deep ring; plus the codebook blocks a
 // workgroup's rows can touch.
 bool make_qplan(uint32_t M, uint32_t K, uint32_t ntok, uint32_t rpc, QPlan& out) {
-    const uint32_t nch = K >> 5, nstep = (nch + 63) / 64, nchp = nstep * 64, cu = vq_ncu();
+    const uint32_t nch = K >> 5, nstep = (nch + 63) / 64, nchp = nstep * 64, cu = cu_count();
     bool found = false;
     double best = 0.0;
     for (uint32_t R = 2; R >= 1; --R) {
