@@ -5,8 +5,8 @@
 // A plan fixes the tiles per wave T (4 with at most 8 waves per workgroup, 2
 // or 1 with at most 16: the register budget of T), the split of a
 // workgroup's waves into P K-parts (P divides the number of 128-k spans) and
-// Q row-group lanes (Q cut to the row groups a CU has), the row groups per
-// workgroup (in rounds of Q) and the ring depth D.
+// Q row-group lanes (Q cut to the row groups a CU has) and the row groups per
+// workgroup (in rounds of Q).
 // Cost = the busiest CU's weight bytes (workgroups it runs x waves x padded
 // steps x T), times a latency factor when a CU has less than ~48 KiB of loads
 // in flight. All tokens (up to 16) go in one pass.
@@ -22,45 +22,45 @@ constexpr size_t kLdsMax = 160 * 1024;
 bool make_plan(uint32_t M, uint32_t K, uint32_t G, uint32_t ntok, Int4Cfg cfg, mfma::Plan& out) {
     (void)ntok;
     const uint32_t nspan = K / 128, ntiles = (M + mfma::kTile - 1) / mfma::kTile, cu = cu_count();
-    // cfg.unroll: 0 = automatic, D (2, 3) or 10 * T + D; cfg.rows: K parts P (0 = automatic)
-    uint32_t fT = 0, fD = 0;
+    // cfg.unroll: 0 = automatic, or 10 * T + 2 (ring depth 2); cfg.rows: K parts P (0 = automatic)
+    uint32_t fT = 0;
     if (cfg.unroll >= 10) {
         fT = (uint32_t)cfg.unroll / 10;
-        fD = (uint32_t)cfg.unroll % 10;
-    } else if (cfg.unroll > 0) {
-        fD = (uint32_t)cfg.unroll;
+        if (cfg.unroll % 10 != 2) return false;
+    } else if (cfg.unroll != 0 && cfg.unroll != 2) {
+        return false;
     }
     if (fT && fT != 1 && fT != 2 && fT != 4) return false;
-    if (fD && fD != 2 && fD != 3) return false;
     bool found = false;
     double best = 0.0;
     for (uint32_t T : {4u, 2u, 1u}) {
         if (fT && T != fT) continue;
-        const uint32_t D = fD ? fD : 2;
-        if (D == 3 && T != 1) continue;
-        const uint32_t wmax = mfma::max_waves(G, T, D);
+        const uint32_t wmax = mfma::max_waves(G, T);
         const uint32_t ngroups = (ntiles + T - 1) / T;
         for (uint32_t P = 1; P <= wmax; ++P) {
             if (nspan % P) continue;
             if (cfg.rows > 0 && (uint32_t)cfg.rows != P) continue;
             // Q is cut to the row groups a CU has (no idle lanes)
             const uint32_t qmax = wmax / P, J = nspan / P;
+            const uint32_t J8 = (J + mfma::kWin - 1) / mfma::kWin * mfma::kWin;
             const uint32_t per_cu = (ngroups + cu - 1) / cu;
             const uint32_t rounds = (per_cu + qmax - 1) / qmax;
             const uint32_t Q = (per_cu + rounds - 1) / rounds, waves = P * Q;
             const uint32_t groups_wg = rounds * Q;
             const uint32_t nwg = (ngroups + groups_wg - 1) / groups_wg;
-            const uint32_t nreal = rounds * J;
-            const uint32_t nsteps = (nreal + D - 1) / D * D;
+            const uint32_t body = 2 * mfma::kWin;
+            const uint32_t nsteps = (rounds * J8 + body - 1) / body * body;
             const size_t lds = mfma::lds_part(waves, T, rounds, P);
             if (lds > kLdsMax) continue;
-            const double inflight = (double)waves * D * T;  // KiB per CU
-            const double cost = (double)((nwg + cu - 1) / cu) * waves * nsteps * T *
+            // padding steps move no bytes but take issue slots
+            const double steps = rounds * J + 0.3 * (nsteps - rounds * J);
+            const double inflight = (double)waves * 2 * T;  // KiB per CU
+            const double cost = (double)((nwg + cu - 1) / cu) * waves * steps * T *
                                 (inflight < 48.0 ? 48.0 / inflight : 1.0) * (P > 1 ? 1.02 : 1.0);
             if (!found || cost < best) {
                 found = true;
                 best = cost;
-                out = mfma::Plan{T, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, waves, lds};
+                out = mfma::Plan{T, P, Q, J, J8, rounds, groups_wg, nwg, nsteps, waves, lds};
             }
         }
     }
@@ -105,10 +105,10 @@ hipError_t launch_int4_mfma(const uint32_t* W, const uint16_t* S, const uint16_t
     a.P = pl.P;
     a.Q = pl.Q;
     a.J = pl.J;
+    a.J8 = pl.J8;
     a.ngroups = ((M + mfma::kTile - 1) / mfma::kTile + pl.T - 1) / pl.T;
     a.groups_wg = pl.groups_wg;
     a.rounds = pl.rounds;
-    a.nreal = pl.nreal;
     a.nsteps = pl.nsteps;
     const bool bf = meta_kind == 1;
     if (G == 32) return launch_mfma_g32(a, pl, interleaved, bf, s);

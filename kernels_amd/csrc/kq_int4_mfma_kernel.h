@@ -46,12 +46,21 @@
 // ... ("rounds"). The P partial tiles of a round are summed in LDS in a fixed
 // order (deterministic).
 //
+// Scale/bias: loaded once per window of 8 spans (each lane holds two spans
+// of its row; ds_bpermute hands a span's values to every lane of the row),
+// since per-span loads of 2-16 bytes from 16 rows cost more than the weights.
+//
 // Pipelining: each wave streams its (row group, span) steps through a ring of
-// D register slots. Every load is unconditional (rows past the end and
-// padding steps are clamped to valid addresses, their results discarded) and
-// is first used by the compute of its own step, so the waitcnt pass sees one
-// straight sequence and waits for exactly one slot at a time.
+// two register slots. Every load is unconditional: rows past the end are
+// clamped to valid addresses (results discarded), and padding steps (a part
+// padded to whole windows, the last round padded to the loop body) load out
+// of the descriptors' range -- zeros, which add exactly nothing, and no
+// memory traffic. Each load is first used by the compute of its own step, so
+// the waitcnt pass sees one straight sequence and waits for exactly one slot
+// at a time.
 #pragma once
+#include <type_traits>
+
 #include "kq_device.h"
 #include "kq_internal.h"
 
@@ -68,22 +77,22 @@ struct Args {
     void* Y;            // [ntok][M]
     uint32_t M, K, ntok, y_f32;
     uint32_t gpr;                // quant groups per row
-    uint32_t P, Q, J;            // K parts, row-group lanes, spans per part
+    uint32_t P, Q, J, J8;        // K parts, row-group lanes, spans per part (J8: padded to windows)
     uint32_t ngroups;            // row groups (T tiles each) in total
     uint32_t groups_wg, rounds;  // row groups per workgroup (= rounds * Q)
-    uint32_t nreal, nsteps;      // steps per wave (rounds * J), padded to D
+    uint32_t nsteps;             // steps per wave (rounds * J8), padded to two windows
 };
 
 // Launch plan chosen on the host.
 struct Plan {
-    uint32_t T, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, waves;
+    uint32_t T, P, Q, J, J8, rounds, groups_wg, nwg, nsteps, waves;
     size_t lds;
 };
 
 // Waves per workgroup that the register budget of (G, T, D) allows without
 // spills: 16 waves leave 128 registers per lane, 8 leave 256.
-__host__ __device__ constexpr uint32_t max_waves(uint32_t G, uint32_t T, uint32_t D) {
-    return T == 4 ? 8 : (G == 32 && (T == 2 || D == 3)) ? 8 : 16;
+__host__ __device__ constexpr uint32_t max_waves(uint32_t G, uint32_t T) {
+    return T >= 2 || G == 32 ? 8 : 16;
 }
 
 __host__ __device__ inline size_t lds_part(uint32_t waves, uint32_t T, uint32_t rounds, uint32_t P) {
@@ -125,25 +134,6 @@ template <>
 struct Meta<4, false> {
     u32x2 s, b;
 };
-
-template <int NG, bool SB>
-__device__ __forceinline__ void load_meta(Meta<NG, SB>& m, rsrc_t rs, rsrc_t rb, uint32_t vo,
-                                          uint32_t so) {
-    if constexpr (SB) {
-        if constexpr (NG == 1) m.v = __builtin_amdgcn_raw_buffer_load_b32(rs, vo, so, 0);
-        else if constexpr (NG == 2) m.v = __builtin_amdgcn_raw_buffer_load_b64(rs, vo, so, 0);
-        else m.v = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, so, 0);
-    } else if constexpr (NG == 1) {
-        m.s = __builtin_amdgcn_raw_buffer_load_b16(rs, vo, so, 0);
-        m.b = __builtin_amdgcn_raw_buffer_load_b16(rb, vo, so, 0);
-    } else if constexpr (NG == 2) {
-        m.s = __builtin_amdgcn_raw_buffer_load_b32(rs, vo, so, 0);
-        m.b = __builtin_amdgcn_raw_buffer_load_b32(rb, vo, so, 0);
-    } else {
-        m.s = __builtin_amdgcn_raw_buffer_load_b64(rs, vo, so, 0);
-        m.b = __builtin_amdgcn_raw_buffer_load_b64(rb, vo, so, 0);
-    }
-}
 
 // Low 16 bits of `raw` as a float (fp16 or bf16 bits).
 template <bool BF>
@@ -244,20 +234,112 @@ struct Cursor {
     }
 };
 
-template <int GM, bool SB, int T>
+// Scale/bias of a window of kWin spans as loaded: lane (row n, group kg)
+// holds spans 2kg, 2kg + 1 of the window, so one instruction reads 8 spans'
+// worth of each of 16 rows (32-128 contiguous bytes per row, instead of 2-16
+// per span). At each span the values are fetched from the owning lane with
+// ds_bpermute (no LDS allocation).
+constexpr int kWin = 8;
+template <int NG, bool SB>
+struct MWin;
+template <>
+struct MWin<1, true> {
+    u32x2 a;  // 2 spans x 1 dword
+};
+template <>
+struct MWin<2, true> {
+    u32x4 a;  // 2 spans x 2 dwords
+};
+template <>
+struct MWin<4, true> {
+    u32x4 a, c;  // span 0, span 1: 4 dwords each
+};
+template <>
+struct MWin<1, false> {
+    uint32_t s, b;  // 2 spans x 1 half
+};
+template <>
+struct MWin<2, false> {
+    u32x2 s, b;  // 2 spans x 2 halves
+};
+template <>
+struct MWin<4, false> {
+    u32x4 s, b;  // 2 spans x 4 halves
+};
+
+template <int NG, bool SB>
+__device__ __forceinline__ void load_mwin(MWin<NG, SB>& m, rsrc_t rs, rsrc_t rb, uint32_t vo) {
+    if constexpr (SB) {
+        if constexpr (NG == 1) m.a = __builtin_amdgcn_raw_buffer_load_b64(rs, vo, 0, 0);
+        else if constexpr (NG == 2) m.a = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, 0, 0);
+        else {
+            m.a = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, 0, 0);
+            m.c = __builtin_amdgcn_raw_buffer_load_b128(rs, vo + 16, 0, 0);
+        }
+    } else if constexpr (NG == 1) {
+        m.s = __builtin_amdgcn_raw_buffer_load_b32(rs, vo, 0, 0);
+        m.b = __builtin_amdgcn_raw_buffer_load_b32(rb, vo, 0, 0);
+    } else if constexpr (NG == 2) {
+        m.s = __builtin_amdgcn_raw_buffer_load_b64(rs, vo, 0, 0);
+        m.b = __builtin_amdgcn_raw_buffer_load_b64(rb, vo, 0, 0);
+    } else {
+        m.s = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, 0, 0);
+        m.b = __builtin_amdgcn_raw_buffer_load_b128(rb, vo, 0, 0);
+    }
+}
+
+__device__ __forceinline__ uint32_t bperm(uint32_t addr, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_ds_bpermute((int)addr, (int)v);
+}
+
+// Meta of window span R for this lane's row; ba = 4 * (n + 16 * (R / 2)).
+template <int NG, bool SB, int R>
+__device__ __forceinline__ Meta<NG, SB> meta_at(const MWin<NG, SB>& w, uint32_t ba) {
+    constexpr int SUB = R & 1;
+    Meta<NG, SB> m;
+    if constexpr (SB) {
+        if constexpr (NG == 1) m.v = bperm(ba, SUB ? w.a.y : w.a.x);
+        else if constexpr (NG == 2) m.v = u32x2{bperm(ba, w.a[2 * SUB]), bperm(ba, w.a[2 * SUB + 1])};
+        else {
+            const u32x4 src = SUB ? w.c : w.a;
+            m.v = u32x4{bperm(ba, src.x), bperm(ba, src.y), bperm(ba, src.z), bperm(ba, src.w)};
+        }
+    } else if constexpr (NG == 1) {
+        m.s = (uint16_t)(bperm(ba, w.s) >> (16 * SUB));
+        m.b = (uint16_t)(bperm(ba, w.b) >> (16 * SUB));
+    } else if constexpr (NG == 2) {
+        m.s = bperm(ba, w.s[SUB]);
+        m.b = bperm(ba, w.b[SUB]);
+    } else {
+        m.s = u32x2{bperm(ba, w.s[2 * SUB]), bperm(ba, w.s[2 * SUB + 1])};
+        m.b = u32x2{bperm(ba, w.b[2 * SUB]), bperm(ba, w.b[2 * SUB + 1])};
+    }
+    return m;
+}
+
+template <int T>
 struct Slot {
     u32x4 w[T];
-    Meta<128 / GM, SB> m[T];
     u32x4 x[4];
 };
 
-template <int GM, bool SB, bool BF, int T, int D, int WAVES>
+template <int F, typename Fn>
+__device__ __forceinline__ void static_for(Fn&& f) {
+    if constexpr (F > 0) {
+        static_for<F - 1>(f);
+        f(std::integral_constant<int, F - 1>{});
+    }
+}
+
+template <int GM, bool SB, bool BF, int T, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
-    constexpr int NG = 128 / GM;       // quant groups per span
-    constexpr int NP = (NG + 1) / 2;   // group pairs (correction MFMAs) per span
-    constexpr int PER = 4 / NG;        // MFMAs per group
+    constexpr int NG = 128 / GM;         // quant groups per span
+    constexpr int NP = (NG + 1) / 2;     // group pairs (correction MFMAs) per span
+    constexpr int PER = 4 / NG;          // MFMAs per group
     constexpr uint32_t MB = SB ? 4 : 2;  // meta bytes per group (per array)
-    using SlotT = Slot<GM, SB, T>;
+    constexpr int D = 2;                 // ring depth (steps)
+    constexpr int U = 2 * kWin;          // steps per loop body (two meta windows)
+    using SlotT = Slot<T>;
 
     extern __shared__ __align__(16) unsigned char smem[];
     float* part = reinterpret_cast<float*>(smem);
@@ -275,6 +357,7 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
     const rsrc_t rS = make_rsrc(A.S, M * A.gpr * MB);
     const rsrc_t rB = make_rsrc(SB ? A.S : A.B, M * A.gpr * MB);
     const rsrc_t rX = make_rsrc(A.X, A.ntok * K * 2);
+    constexpr uint32_t kOOB = 0x80000000u;  // past every descriptor's range: the load reads zeros
 
     // lane-constant parts of the x addresses (token n, clamped into the batch)
     uint32_t xvo[4];
@@ -283,11 +366,14 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) xvo[j] = t * K * 2 + xword<GM>(j, kg) * 16;
     }
+    uint32_t ba[4];  // ds_bpermute addresses of lane (n, group k)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ba[k] = 4 * (n + 16 * k);
 
     // lane-constant parts of the weight / meta addresses of the current issue round
     uint32_t wvo[T], mvo[T];
     uint32_t cur_rg = 0xFFFFFFFFu;
-    auto set_rows = [&](uint32_t rg) {
+    auto set_rows = [&](uint32_t rg) __attribute__((always_inline)) {
         cur_rg = rg;
 #pragma unroll
         for (int i = 0; i < T; ++i) {
@@ -298,34 +384,53 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
         }
     };
 
-    // ---- prime the ring (one straight sequence of loads)
-    SlotT ring[D];
-    auto issue = [&](SlotT& e, Cursor c) {
-        if (c.round >= A.rounds) {  // padding step: re-read the last real one
-            c.round = A.rounds - 1;
-            c.j = A.J - 1;
-        }
-        uint32_t rg = g0 + c.round * A.Q + q;
+    // ---- the load stream. Steps past a part's J spans (padding to whole
+    // windows) and past the last round load out of range: zeros, which add
+    // nothing (x = 0 and scale/bias = 0), and cost no memory traffic.
+    // named buffers, not arrays: arrays of these (selected by constant
+    // indices after unrolling) have been kept in scratch by the compiler
+    SlotT ring0, ring1;
+    MWin<NG, SB> mwa[T], mwb[T];
+    auto slot = [&](auto k) __attribute__((always_inline)) -> SlotT& {
+        if constexpr (decltype(k)::value == 0) return ring0;
+        else return ring1;
+    };
+    auto mwin = [&](auto b) __attribute__((always_inline)) -> MWin<NG, SB>* {
+        if constexpr (decltype(b)::value == 0) return mwa;
+        else return mwb;
+    };
+    auto issue = [&](SlotT& e, Cursor c, auto win) __attribute__((always_inline)) {
+        const bool ok = c.round < A.rounds && c.j < A.J;
+        uint32_t rg = g0 + (c.round < A.rounds ? c.round : A.rounds - 1) * A.Q + q;
         rg = __builtin_amdgcn_readfirstlane(rg < A.ngroups ? rg : A.ngroups - 1);
         if (rg != cur_rg) set_rows(rg);
         // uniform by construction; readfirstlane keeps it in an SGPR (a scalar
         // offset the compiler thinks divergent becomes a waterfall loop)
-        const uint32_t span = __builtin_amdgcn_readfirstlane(p * A.J + c.j);
+        const uint32_t span = __builtin_amdgcn_readfirstlane(p * A.J + (c.j < A.J ? c.j : A.J - 1));
+        const uint32_t oob = ok ? 0u : kOOB;
+        if constexpr (decltype(win)::value >= 0) {  // first step of a window: its scale/bias
+            const uint32_t j2 = c.j + 2 * kg;
+            const bool lok = c.round < A.rounds && j2 < A.J;
+            const uint32_t lspan = p * A.J + (j2 < A.J ? j2 : A.J - 1);
 #pragma unroll
-        for (int i = 0; i < T; ++i) {
-            e.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rW, wvo[i], span * 64, kNT);
-            load_meta<NG, SB>(e.m[i], rS, rB, mvo[i], span * NG * MB);
+            for (int i = 0; i < T; ++i)
+                load_mwin<NG, SB>(mwin(win)[i], rS, rB,
+                                  mvo[i] + lspan * NG * MB + (lok ? 0u : kOOB));
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) e.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rX, xvo[j], span * 256, 0);
+        for (int i = 0; i < T; ++i)
+            e.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rW, wvo[i] + oob, span * 64, kNT);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            e.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rX, xvo[j] + oob, span * 256, 0);
     };
     Cursor ci{0, 0};
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        issue(ring[d], ci);
-        ci.advance(A.J);
-        __builtin_amdgcn_sched_barrier(0);
-    }
+    issue(ring0, ci, std::integral_constant<int, 0>{});
+    ci.advance(A.J8);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(ring1, ci, std::integral_constant<int, -1>{});
+    ci.advance(A.J8);
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- per-lane constants
     const DequantConsts kc;
@@ -387,8 +492,10 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
         for (int i = 0; i < T; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     };
 
-    // ---- one step: x-only sums, then per tile the group MFMAs and epilogue
-    auto step = [&](const SlotT& e, Cursor c, uint32_t nstep) {
+    // ---- one step: x-only sums, then per tile the group MFMAs and epilogue.
+    // RW = the step's span within its window, B = the window's buffer.
+    auto step = [&](const SlotT& e, Cursor c, auto rw, auto buf) __attribute__((always_inline)) {
+        constexpr int RW = decltype(rw)::value, B = decltype(buf)::value;
         f16x8 xa[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) xa[j] = xperm(e.x[j]);
@@ -397,6 +504,7 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
         for (int j = 0; j < 4; ++j) sums = mma16(ac[j / PER], xa[j], sums);
 #pragma unroll
         for (int i = 0; i < T; ++i) {
+            const Meta<NG, SB> m = meta_at<NG, SB, RW>(mwin(std::integral_constant<int, B>{})[i], ba[RW / 2]);
             uint32_t w[4] = {e.w[i].x, e.w[i].y, e.w[i].z, e.w[i].w};
             regroup<GM>(w);
             f32x4 dg[NG];
@@ -408,40 +516,51 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
             }
 #pragma unroll
             for (int gi = 0; gi < NG; ++gi) {
-                const float s = sval<NG, SB, BF>(e.m[i], gi);
+                const float sc = sval<NG, SB, BF>(m, gi);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(s, dg[gi][r], acc[i][r]);
+                for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(sc, dg[gi][r], acc[i][r]);
             }
 #pragma unroll
             for (int pp = 0; pp < NP; ++pp)
                 acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                    sums[pp], bcorr<NG, SB, BF>(e.m[i], pp, hi_grp, want_s, shs, hsel), acc[i], 0, 0, 0);
+                    sums[pp], bcorr<NG, SB, BF>(m, pp, hi_grp, want_s, shs, hsel), acc[i], 0, 0, 0);
         }
-        if (nstep < A.nreal && c.j == A.J - 1) finish(c.round);
+        if (c.round < A.rounds && c.j == A.J8 - 1) finish(c.round);
     };
 
-    // ---- main loop (loads D steps ahead), then the last D steps
+    // ---- main loop: U steps per body (two meta windows, so every buffer
+    // index is a constant), loads D steps ahead; then the last U steps
     Cursor cc{0, 0};
     uint32_t ns = 0;
-    for (; ns + D < A.nsteps; ns += D) {
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            step(ring[d], cc, ns + d);
-            cc.advance(A.J);
-            issue(ring[d], ci);
-            ci.advance(A.J);
+    for (; ns + U < A.nsteps; ns += U) {
+        static_for<U>([&](auto dd) __attribute__((always_inline)) {
+            constexpr int d = decltype(dd)::value;
+            step(slot(std::integral_constant<int, d % D>{}), cc, std::integral_constant<int, d % kWin>{},
+                 std::integral_constant<int, d / kWin>{});
+            cc.advance(A.J8);
+            constexpr int nx = d + D;  // the step issued now, relative to ns
+            issue(slot(std::integral_constant<int, d % D>{}), ci,
+                  std::integral_constant<int, nx % kWin == 0 ? (nx / kWin) % 2 : -1>{});
+            ci.advance(A.J8);
+        });
+    }
+    static_for<U>([&](auto dd) __attribute__((always_inline)) {
+        constexpr int d = decltype(dd)::value;
+        step(slot(std::integral_constant<int, d % D>{}), cc, std::integral_constant<int, d % kWin>{},
+             std::integral_constant<int, d / kWin>{});
+        cc.advance(A.J8);
+        if constexpr (d + D < U) {
+            constexpr int nx = d + D;
+            issue(slot(std::integral_constant<int, d % D>{}), ci,
+                  std::integral_constant<int, nx % kWin == 0 ? (nx / kWin) % 2 : -1>{});
+            ci.advance(A.J8);
         }
-    }
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        step(ring[d], cc, ns + d);
-        cc.advance(A.J);
-    }
+    });
 }
 
-template <int GM, bool SB, bool BF, int T, int D, int WAVES>
+template <int GM, bool SB, bool BF, int T, int WAVES>
 hipError_t go(const Args& a, const Plan& pl, hipStream_t s) {
-    auto kern = int4_mfma<GM, SB, BF, T, D, WAVES>;
+    auto kern = int4_mfma<GM, SB, BF, T, WAVES>;
     if (pl.lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -454,10 +573,9 @@ hipError_t go(const Args& a, const Plan& pl, hipStream_t s) {
 
 template <int GM, bool SB, bool BF>
 hipError_t go_td(const Args& a, const Plan& pl, hipStream_t s) {
-    if (pl.T == 4 && pl.D == 2) return go<GM, SB, BF, 4, 2, max_waves(GM, 4, 2)>(a, pl, s);
-    if (pl.T == 2 && pl.D == 2) return go<GM, SB, BF, 2, 2, max_waves(GM, 2, 2)>(a, pl, s);
-    if (pl.T == 1 && pl.D == 2) return go<GM, SB, BF, 1, 2, max_waves(GM, 1, 2)>(a, pl, s);
-    if (pl.T == 1 && pl.D == 3) return go<GM, SB, BF, 1, 3, max_waves(GM, 1, 3)>(a, pl, s);
+    if (pl.T == 4) return go<GM, SB, BF, 4, max_waves(GM, 4)>(a, pl, s);
+    if (pl.T == 2) return go<GM, SB, BF, 2, max_waves(GM, 2)>(a, pl, s);
+    if (pl.T == 1) return go<GM, SB, BF, 1, max_waves(GM, 1)>(a, pl, s);
     return hipErrorInvalidValue;
 }
 

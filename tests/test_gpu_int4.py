@@ -121,17 +121,18 @@ def test_forced_launch_shapes_agree(gpu, K, parts, depth, M, batch):
     check(got, ref_int4(p), f"P={parts} D={depth} K={K} M={M} b={batch}")
 
 
-# (K parts P, 10 * tiles per wave T + ring depth D)
-MFMA_PLANS = [(16, 12), (16, 13), (8, 22), (2, 22), (4, 42), (8, 42), (1, 42), (1, 13)]
+# (K parts P, 10 * tiles per wave T + ring depth 2)
+MFMA_PLANS = [(16, 12), (1, 12), (8, 22), (2, 22), (4, 42), (8, 42), (1, 42), (4, 2)]
 
 
 @pytest.mark.parametrize("parts,unroll", MFMA_PLANS)
 @pytest.mark.parametrize("M,batch", [(1000, 1), (257, 5), (9600, 3)])
 def test_mfma_forced_plans_agree(gpu, parts, unroll, M, batch):
-    """Every (K parts, tiles per wave, ring depth) plan of the matrix-core
-    path gives the oracle's result: padding steps, clamped rows, idle lanes
-    and several rounds per workgroup (M = 9600: 600 tiles) included
-    (K = 4096: 32 spans)."""
+    """Every (K parts, tiles per wave) plan of the matrix-core path gives the
+    oracle's result: parts padded to whole scale/bias windows (P = 16: 2
+    spans per part, 6 padding steps), clamped rows, idle lanes and several
+    rounds per workgroup (M = 9600: 600 tiles) included (K = 4096: 32
+    spans)."""
     p = gen.int4_problem(M, 4096, 64, batch=batch, seed=parts * 100 + unroll + M)
     got = run_int4(p, gpu, path=kq.PATH_MFMA, rows=parts, unroll=unroll)
     check(got, ref_int4(p), f"mfma P={parts} T,D={unroll} M={M} b={batch}")
@@ -144,4 +145,7 @@ def test_mfma_forced_plan_unsupported(gpu):
     assert e.value.status == kq.KQ_EUNSUPPORTED
     with pytest.raises(kq.KQError) as e:
         run_int4(p, gpu, path=kq.PATH_MFMA, rows=16, unroll=42)  # T = 4 has 8 waves
+    assert e.value.status == kq.KQ_EUNSUPPORTED
+    with pytest.raises(kq.KQError) as e:
+        run_int4(p, gpu, path=kq.PATH_MFMA, rows=4, unroll=13)  # ring depth is 2
     assert e.value.status == kq.KQ_EUNSUPPORTED
