@@ -50,7 +50,7 @@ bool make_plan(uint32_t M, uint32_t K, uint32_t G, uint32_t ntok, Int4Cfg cfg, m
             const uint32_t nwg = (ngroups + groups_wg - 1) / groups_wg;
             const uint32_t body = 2 * mfma::kWin;
             const uint32_t nsteps = (rounds * J8 + body - 1) / body * body;
-            const size_t lds = mfma::lds_part(waves, T, rounds, P);
+            const size_t lds = mfma::lds_part(waves, T, rounds, P) + mfma::lds_wstage(waves, T);
             if (lds > kLdsMax) continue;
             // padding steps move no bytes but take issue slots
             const double steps = rounds * J + 0.3 * (nsteps - rounds * J);
@@ -110,6 +110,7 @@ hipError_t launch_int4_mfma(const uint32_t* W, const uint16_t* S, const uint16_t
     a.groups_wg = pl.groups_wg;
     a.rounds = pl.rounds;
     a.nsteps = pl.nsteps;
+    a.part_bytes = (uint32_t)mfma::lds_part(pl.waves, pl.T, pl.rounds, pl.P);
     const bool bf = meta_kind == 1;
     if (G == 32) return launch_mfma_g32(a, pl, interleaved, bf, s);
     if (G == 64) return launch_mfma_g64(a, pl, interleaved, bf, s);

@@ -81,6 +81,7 @@ struct Args {
     uint32_t ngroups;            // row groups (T tiles each) in total
     uint32_t groups_wg, rounds;  // row groups per workgroup (= rounds * Q)
     uint32_t nsteps;             // steps per wave (rounds * J8), padded to two windows
+    uint32_t part_bytes;         // LDS of the K-part reduction (the weight staging follows)
 };
 
 // Launch plan chosen on the host.
@@ -97,6 +98,10 @@ __host__ __device__ constexpr uint32_t max_waves(uint32_t G, uint32_t T) {
 
 __host__ __device__ inline size_t lds_part(uint32_t waves, uint32_t T, uint32_t rounds, uint32_t P) {
     return P > 1 ? (size_t)(rounds > 1 ? 2 : 1) * waves * T * 4 * 64 * 4 : 0;
+}
+// Per wave: the span-pair staging of its T tiles (16 rows x 128 bytes each).
+__host__ __device__ inline size_t lds_wstage(uint32_t waves, uint32_t T) {
+    return (size_t)waves * T * 2048;
 }
 
 
@@ -317,9 +322,15 @@ __device__ __forceinline__ Meta<NG, SB> meta_at(const MWin<NG, SB>& w, uint32_t 
     return m;
 }
 
+// Ring slots. Even steps also carry the weights of a span pair: per tile two
+// loads of 8 rows x 128 contiguous bytes (a lane: row 8h + l/8, 16-byte
+// chunk (l % 8) ^ (row % 8) of the pair).
 template <int T>
-struct Slot {
-    u32x4 w[T];
+struct SlotE {
+    u32x4 w[T][2];
+    u32x4 x[4];
+};
+struct SlotO {
     u32x4 x[4];
 };
 
@@ -339,7 +350,7 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
     constexpr uint32_t MB = SB ? 4 : 2;  // meta bytes per group (per array)
     constexpr int D = 2;                 // ring depth (steps)
     constexpr int U = 2 * kWin;          // steps per loop body (two meta windows)
-    using SlotT = Slot<T>;
+
 
     extern __shared__ __align__(16) unsigned char smem[];
     float* part = reinterpret_cast<float*>(smem);
@@ -352,6 +363,8 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
     const uint32_t p = wave % A.P, q = wave / A.P;
     const uint32_t n = lane & 15, kg = lane >> 4;
     const uint32_t g0 = blockIdx.x * A.groups_wg;
+    // this wave's span-pair staging: per tile 16 rows x 128 bytes (swizzled)
+    unsigned char* wst = smem + A.part_bytes + (size_t)wave * T * 2048;
 
     const rsrc_t rW = make_rsrc(A.W, M * (K / 2));
     const rsrc_t rS = make_rsrc(A.S, M * A.gpr * MB);
@@ -370,8 +383,14 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) ba[k] = 4 * (n + 16 * k);
 
+    // LDS read offsets of (row n, chunk 4s + kg) for span s of a pair
+    uint32_t rdo[2];
+#pragma unroll
+    for (int sp = 0; sp < 2; ++sp)
+        rdo[sp] = (n >> 3) * 1024 + ((((n & 7) << 3) | ((4 * sp + kg) ^ (n & 7))) * 16);
+
     // lane-constant parts of the weight / meta addresses of the current issue round
-    uint32_t wvo[T], mvo[T];
+    uint32_t wvo[T][2], mvo[T];
     uint32_t cur_rg = 0xFFFFFFFFu;
     auto set_rows = [&](uint32_t rg) __attribute__((always_inline)) {
         cur_rg = rg;
@@ -379,8 +398,13 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
         for (int i = 0; i < T; ++i) {
             uint32_t row = rg * (16 * T) + 16 * i + n;
             row = row < M ? row : M - 1;
-            wvo[i] = row * (K / 2) + kg * 16;
             mvo[i] = row * A.gpr * MB;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t r = rg * (16 * T) + 16 * i + 8 * h + (lane >> 3);
+                r = r < M ? r : M - 1;
+                wvo[i][h] = r * (K / 2) + (((lane & 7) ^ ((lane >> 3) & 7)) * 16);
+            }
         }
     };
 
@@ -389,9 +413,10 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
     // nothing (x = 0 and scale/bias = 0), and cost no memory traffic.
     // named buffers, not arrays: arrays of these (selected by constant
     // indices after unrolling) have been kept in scratch by the compiler
-    SlotT ring0, ring1;
+    SlotE<T> ring0;
+    SlotO ring1;
     MWin<NG, SB> mwa[T], mwb[T];
-    auto slot = [&](auto k) __attribute__((always_inline)) -> SlotT& {
+    auto slot = [&](auto k) __attribute__((always_inline)) -> auto& {
         if constexpr (decltype(k)::value == 0) return ring0;
         else return ring1;
     };
@@ -399,7 +424,7 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
         if constexpr (decltype(b)::value == 0) return mwa;
         else return mwb;
     };
-    auto issue = [&](SlotT& e, Cursor c, auto win) __attribute__((always_inline)) {
+    auto issue = [&](auto& e, Cursor c, auto win) __attribute__((always_inline)) {
         const bool ok = c.round < A.rounds && c.j < A.J;
         uint32_t rg = g0 + (c.round < A.rounds ? c.round : A.rounds - 1) * A.Q + q;
         rg = __builtin_amdgcn_readfirstlane(rg < A.ngroups ? rg : A.ngroups - 1);
@@ -417,9 +442,16 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
                 load_mwin<NG, SB>(mwin(win)[i], rS, rB,
                                   mvo[i] + lspan * NG * MB + (lok ? 0u : kOOB));
         }
+        if constexpr (std::is_same_v<std::decay_t<decltype(e)>, SlotE<T>>) {
+            // the pair (span, span + 1); its offset goes in the lane offset, so
+            // the range check covers a pair running past the last row
+            const uint32_t po = span * 64 + oob;
 #pragma unroll
-        for (int i = 0; i < T; ++i)
-            e.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rW, wvo[i] + oob, span * 64, kNT);
+            for (int i = 0; i < T; ++i)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    e.w[i][h] = __builtin_amdgcn_raw_buffer_load_b128(rW, wvo[i][h] + po, 0, kNT);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             e.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rX, xvo[j] + oob, span * 256, 0);
@@ -494,8 +526,15 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
 
     // ---- one step: x-only sums, then per tile the group MFMAs and epilogue.
     // RW = the step's span within its window, B = the window's buffer.
-    auto step = [&](const SlotT& e, Cursor c, auto rw, auto buf) __attribute__((always_inline)) {
-        constexpr int RW = decltype(rw)::value, B = decltype(buf)::value;
+    auto step = [&](const auto& e, Cursor c, auto rw, auto buf) __attribute__((always_inline)) {
+        constexpr int RW = decltype(rw)::value, B = decltype(buf)::value, SP = RW & 1;
+        if constexpr (SP == 0) {  // stage the pair's weights in LDS (this wave's area)
+#pragma unroll
+            for (int i = 0; i < T; ++i)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    *reinterpret_cast<u32x4*>(wst + i * 2048 + h * 1024 + lane * 16) = e.w[i][h];
+        }
         f16x8 xa[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) xa[j] = xperm(e.x[j]);
@@ -505,7 +544,8 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
 #pragma unroll
         for (int i = 0; i < T; ++i) {
             const Meta<NG, SB> m = meta_at<NG, SB, RW>(mwin(std::integral_constant<int, B>{})[i], ba[RW / 2]);
-            uint32_t w[4] = {e.w[i].x, e.w[i].y, e.w[i].z, e.w[i].w};
+            const u32x4 wv = *reinterpret_cast<const u32x4*>(wst + i * 2048 + rdo[SP]);
+            uint32_t w[4] = {wv.x, wv.y, wv.z, wv.w};
             regroup<GM>(w);
             f32x4 dg[NG];
 #pragma unroll
