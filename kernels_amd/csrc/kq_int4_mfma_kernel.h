@@ -30,13 +30,19 @@
 //   x is A (rows = tokens), W is B (columns = weight rows), so D lane L holds
 //   tokens 4(L/16)+r of weight row L%16; the accumulators keep that layout.
 //
-// Memory: a lane loads 16 B (a 128-k "span" has 16 words per row; lane group
-// L/16 takes words 4(L/16)..+3), so one wave instruction reads 64 B from each
-// of 16 rows. A wave owns T row tiles (16T rows) and one K part; per span it
-// loads the T tiles' words and scale/bias, and x of the span (four 16-B loads
-// per lane, L1/L2-resident, permuted in registers to the dequant order). All
-// loads are buffer loads: the lane-constant part of an address sits in a VGPR
-// and the span offset in an SGPR, so addressing costs no vector instructions.
+// Memory: an MFMA lane needs 16 B (4 words) of one row per 128-k "span", so
+// a direct load would read 64 B from each of 16 rows per instruction -- an
+// access shape that streams ~20% below the full rate. Weights are therefore
+// loaded as span pairs: one instruction reads 128 B (two spans) from each of
+// 8 rows (lane L: row L/8, 16-byte chunk L%8), two instructions per 16-row
+// tile. The pair goes through a per-wave LDS stage of 16 rows x 128 B with
+// the chunk index XOR-swizzled by the row (conflict-free writes and reads)
+// and is read back in the MFMA operand layout, one span per step. x of the
+// span comes with four 16-B loads per lane (L1/L2-resident), permuted in
+// registers to the dequant order. All loads are buffer loads: the
+// lane-constant part of an address sits in a VGPR and the span offset in an
+// SGPR (or in the lane offset, where it must be range-checked), so
+// addressing costs no vector instructions.
 // For the per-group epilogue each MFMA's 32 k must lie in one quant group;
 // v_permlane{32,16}_swap arrange that (G = 64: swap (r0,r2), (r1,r3) between
 // the wave halves; G = 32: then permlane16 swaps of (r0,r1), (r2,r3)).

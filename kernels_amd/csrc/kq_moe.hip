@@ -13,13 +13,13 @@
 //    agent-scope atomics: they bypass the non-coherent per-XCD L2), so no
 //    L2 write-back fence is needed -- measured ~2 us cheaper per block than a
 //    release fence, and cheaper than a separate selection launch.
-// 2. moe_gate_up_k: persistent workgroups take (expert, 2-row group) items
-//    from the plan; every workgroup stages the tokens' x in LDS once; a wave
-//    streams its items through a 2-deep ring of register slots (unconditional
-//    clamped loads, dequant at use), and each item is applied to every token
-//    slot that chose its expert -- so each selected expert's rows are read
-//    once per call. A half-wave owns the gate row, the other half the up row
-//    (K = 2880 = 90 chunks -> 3 per lane), so SwiGLU sees the two half sums.
+// 2. moe_gate_up_k: grid (16-row tile, u); workgroup (x, u) takes the u-th
+//    distinct selected expert of the plan and issues all of its loads (4 gate
+//    + 4 up rows per wave, clamped, dequant at use) in one round trip; the
+//    rows stay in registers and are applied to every token slot that chose
+//    the expert -- so each selected expert's rows are read once per call. A
+//    half-wave owns the gate row, the other half the up row (K = 2880 = 90
+//    chunks -> 3 per lane), so SwiGLU sees the two half sums.
 // 3. moe_down_k: a workgroup owns 8 output rows for every selected expert:
 //    (expert, 4-row) items in a 2-deep ring per wave, per-slot
 //    wgt * (down . h + bias) kept in LDS and summed in slot order --
@@ -529,9 +529,6 @@ __global__ __launch_bounds__(kGuThreads) void moe_gate_up_k(
     }
 }
 
-// ---------------------------------------------------------------------------
-// 3. gather + down + weighted combine
-// ---------------------------------------------------------------------------
 // ---------------------------------------------------------------------------
 // 3. gather + down + weighted combine
 // ---------------------------------------------------------------------------
