@@ -102,45 +102,67 @@ __host__ __device__ inline size_t vlds_x(uint32_t ntok, uint32_t nchp) {
     return (size_t)ntok * nchp * 72;
 }
 
+// x in LDS: per (step s, token t) one 4608-byte block -- four planes of the
+// 64 lanes' permuted pairs (plane jw = word jw of each chunk, 16 B per lane)
+// and the 64 lanes' (sum, offset constant) -- at (s * NB + t) * kXBlk. A
+// lane's reads of an item are one base VGPR plus immediate offsets.
+constexpr uint32_t kXBlk = 4608;
+constexpr int kXr = 8;  // x words a thread stages per pass (one pass up to 8 x threads)
+
 template <int NB, int R, int D, bool SB, bool BF>
 __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const uint32_t nch = A.nch, nchp = A.nchp, nw = A.K >> 3;
-    u32x4* xp = reinterpret_cast<u32x4*>(smem);                             // [NB][4][nchp]
-    float2* xk = reinterpret_cast<float2*>(smem + (size_t)NB * nchp * 64);  // [NB][nchp]
-    float* part = reinterpret_cast<float*>(smem + vlds_x(NB, nchp));        // [2][waves][R*NB]
+    constexpr uint32_t MB = SB ? 4 : 2;  // metadata bytes per group and array
+    constexpr uint32_t kOOB = 0x80000000u;  // past every descriptor's range: loads read zeros
+    const uint32_t nch = A.nch, nchp = A.nchp, nw = A.K >> 3, nstep = nchp >> 6;
+    float* part = reinterpret_cast<float*>(smem + vlds_x(NB, nchp));  // [rounds][waves][R*NB]
 
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
-    const int lane = tid & 63;
-    const uint32_t wave = tid >> 6, p = wave % A.P, q = wave / A.P;
+    const uint32_t lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t p = wave % A.P, q = wave / A.P;
     const uint32_t g0 = blockIdx.x * A.groups_wg;
     const uint32_t last_group = A.ngroups - 1, last_row = A.M - 1;
-    const u32x4* W4 = reinterpret_cast<const u32x4*>(A.W);
 
-    // ---- 1. x staging loads first (vmcnt retires in order)
+    // Descriptors based at this workgroup's first row: every offset is small,
+    // and the range checks turn the lanes past a partial last step into
+    // zero loads that move no bytes.
+    const uint32_t row0 = g0 * R;
+    const uint32_t rows_wg = min(A.groups_wg * R, A.M - row0);
+    const uint32_t rowb = A.K >> 1, metab = A.gpr * MB;
+    const rsrc_t rW = make_rsrc(reinterpret_cast<const unsigned char*>(A.W) + (size_t)row0 * rowb,
+                                rows_wg * rowb);
+    const rsrc_t rS = make_rsrc(reinterpret_cast<const unsigned char*>(A.S) + (size_t)row0 * metab,
+                                rows_wg * metab);
+    const rsrc_t rB = make_rsrc(reinterpret_cast<const unsigned char*>(SB ? A.S : A.B) +
+                                    (size_t)row0 * metab, rows_wg * metab);
+    const rsrc_t rX = make_rsrc(A.X, NB * A.K * 2);
+
+    // ---- 1. x staging loads first (vmcnt retires in order), all in one pass
     const uint32_t xtotal = NB * nw;
-    const u32x4* X4 = reinterpret_cast<const u32x4*>(A.X);
-    constexpr int kXr = 2;
     u32x4 sv[kXr];
-    auto x_load = [&](uint32_t w0) {
+    auto x_load = [&](uint32_t w0) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < kXr; ++r) {
+            if (w0 + r * nthr >= xtotal) break;  // uniform
             const uint32_t w = w0 + r * nthr + tid;
-            sv[r] = X4[w < xtotal ? w : xtotal - 1];
+            sv[r] = __builtin_amdgcn_raw_buffer_load_b128(rX, w < xtotal ? w * 16 : kOOB, 0, 0);
         }
     };
-    auto x_store = [&](uint32_t w0) {
+    auto x_store = [&](uint32_t w0) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < kXr; ++r) {
+            if (w0 + r * nthr >= xtotal) break;  // uniform
             const uint32_t w = w0 + r * nthr + tid;
             float s, c;
             word_consts(sv[r], s, c);
             s = quad_sum(s);
             c = quad_sum(c);
             if (w < xtotal) {
-                const uint32_t t = w / nw, wi = w - t * nw, ch = wi >> 2, j = wi & 3;
-                xp[(t * 4 + j) * nchp + ch] = pair_perm(sv[r]);
-                if (j == 0) xk[t * nchp + ch] = make_float2(s, c);
+                const uint32_t t = w / nw, wi = w - t * nw, ch = wi >> 2, jw = wi & 3;
+                unsigned char* blk = smem + ((ch >> 6) * NB + t) * kXBlk;
+                *reinterpret_cast<u32x4*>(blk + jw * 1024 + (ch & 63) * 16) = pair_perm(sv[r]);
+                if (jw == 0) *reinterpret_cast<float2*>(blk + 4096 + (ch & 63) * 8) = make_float2(s, c);
             }
         }
     };
@@ -148,24 +170,30 @@ __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 2. prime the ring
+    // lane offsets: full steps, and the last step (OOB past the row's end)
+    const uint32_t cl = (nstep - 1) * 64 + lane;
+    const uint32_t vw_full = lane * 16, vw_last = cl < nch ? lane * 16 : kOOB;
+    const uint32_t vm_full = (lane >> A.cshift) * MB, vm_last = cl < nch ? vm_full : kOOB;
     VSlot<R, SB> ring[D];
-    auto issue = [&](VSlot<R, SB>& e, Cursor c) {
+    auto issue = [&](VSlot<R, SB>& e, Cursor c) __attribute__((always_inline)) {
         if (c.round >= A.rounds) {  // padding item: re-read the last real one
             c.round = A.rounds - 1;
             c.j = A.J - 1;
         }
         const uint32_t grp = min(g0 + c.round * A.Q + q, last_group);
-        const uint32_t ch = min((p * A.J + c.j) * 64 + lane, nch - 1);
+        const uint32_t s = __builtin_amdgcn_readfirstlane(p * A.J + c.j);
+        const bool last = s == nstep - 1;
+        const uint32_t vw = last ? vw_last : vw_full, vm = last ? vm_last : vm_full;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t row = min(grp * R + r, last_row);
-            e.w[r] = ldg_nt(W4 + (size_t)row * nch + ch);
-            const size_t gi = (size_t)row * A.gpr + (ch >> A.cshift);
+            const uint32_t rr = __builtin_amdgcn_readfirstlane(min(grp * R + r, last_row) - row0);
+            e.w[r] = __builtin_amdgcn_raw_buffer_load_b128(rW, vw, rr * rowb + s * 1024, kNT);
+            const uint32_t mo = rr * metab + (s * (64u >> A.cshift)) * MB;
             if constexpr (SB) {
-                e.s[r] = reinterpret_cast<const uint32_t*>(A.S)[gi];
+                e.s[r] = __builtin_amdgcn_raw_buffer_load_b32(rS, vm, mo, 0);
             } else {
-                e.s[r] = A.S[gi];
-                e.b[r] = A.B[gi];
+                e.s[r] = __builtin_amdgcn_raw_buffer_load_b16(rS, vm, mo, 0);
+                e.b[r] = __builtin_amdgcn_raw_buffer_load_b16(rB, vm, mo, 0);
             }
         }
     };
@@ -185,10 +213,11 @@ __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
     }
     const uint32_t npad = nchp - nch;
     for (uint32_t i = tid; i < NB * 5 * npad; i += nthr) {
-        const uint32_t t = i / (5 * npad), rem = i - t * 5 * npad, j = rem / npad;
-        const uint32_t ch = nch + (rem - j * npad);
-        if (j < 4) xp[(t * 4 + j) * nchp + ch] = u32x4{0, 0, 0, 0};
-        else xk[t * nchp + ch] = make_float2(0.0f, 0.0f);
+        const uint32_t t = i / (5 * npad), rem = i - t * 5 * npad, jw = rem / npad;
+        const uint32_t ch = nch + (rem - jw * npad);
+        unsigned char* blk = smem + ((ch >> 6) * NB + t) * kXBlk;
+        if (jw < 4) *reinterpret_cast<u32x4*>(blk + jw * 1024 + (ch & 63) * 16) = u32x4{0, 0, 0, 0};
+        else *reinterpret_cast<float2*>(blk + 4096 + (ch & 63) * 8) = make_float2(0.0f, 0.0f);
     }
     __syncthreads();
 
@@ -199,12 +228,12 @@ __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
 #pragma unroll
         for (int t = 0; t < NB; ++t) acc[r][t] = 0.0f;
 
-    auto store = [&](uint32_t row, int t, float v) {
+    auto store = [&](uint32_t row, int t, float v) __attribute__((always_inline)) {
         const size_t o = (size_t)t * A.M + row;
         if (A.y_f32) reinterpret_cast<float*>(A.Y)[o] = v;
         else reinterpret_cast<uint16_t*>(A.Y)[o] = f2h(v);
     };
-    auto finish = [&](uint32_t round) {
+    auto finish = [&](uint32_t round) __attribute__((always_inline)) {
         const uint32_t gl = round * A.Q + q, grp = g0 + gl;
         if (A.P == 1) {
 #pragma unroll
@@ -219,7 +248,9 @@ __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
                 }
             return;
         }
-        float* pw = part + ((size_t)(round & 1) * (A.P * A.Q) + wave) * (R * NB);
+        // K parts: this wave's partial sums of the round go to LDS; all
+        // rounds are summed after the stream (one barrier per launch)
+        float* pw = part + ((size_t)round * (A.P * A.Q) + wave) * (R * NB);
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -228,19 +259,22 @@ __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
                 acc[r][t] = 0.0f;
                 if (lane == 0) pw[r * NB + t] = v;
             }
-        __syncthreads();
-        const float* pr = part + (size_t)(round & 1) * (A.P * A.Q) * (R * NB);
-        const uint32_t nout = A.Q * R * NB;
-        for (uint32_t i = tid; i < nout; i += nthr) {
-            const uint32_t qq = i / (R * NB), rt = i - qq * (R * NB);
-            float v = 0.0f;
-            for (uint32_t pp = 0; pp < A.P; ++pp) v += pr[(qq * A.P + pp) * (R * NB) + rt];
-            const uint32_t gq = round * A.Q + qq, gg = g0 + gq, row = gg * R + rt / NB;
-            if (gq < A.groups_wg && gg < A.ngroups && row < A.M) store(row, rt % NB, v);
-        }
     };
-    auto step = [&](const VSlot<R, SB>& e, Cursor c, uint32_t n) {
-        const uint32_t ch = (p * A.J + c.j) * 64 + lane;
+    const uint32_t vx_lane = lane * 16, vk_lane = 4096 + lane * 8;
+    auto step = [&](const VSlot<R, SB>& e, Cursor c, uint32_t n) __attribute__((always_inline)) {
+        if (n >= A.nreal) return;  // padding to the ring depth (uniform)
+        const uint32_t sb = (p * A.J + c.j) * (NB * kXBlk);
+        const unsigned char* bx = smem + vx_lane + sb;
+        const unsigned char* bk = smem + vk_lane + sb;
+        u32x4 px[NB][4];
+        float2 k2[NB];
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+#pragma unroll
+            for (int jw = 0; jw < 4; ++jw)
+                px[t][jw] = *reinterpret_cast<const u32x4*>(bx + t * kXBlk + jw * 1024);
+            k2[t] = *reinterpret_cast<const float2*>(bk + t * kXBlk);
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const u32x4 d0 = dq4(e.w[r].x, kc), d1 = dq4(e.w[r].y, kc);
@@ -255,17 +289,12 @@ __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
             }
 #pragma unroll
             for (int t = 0; t < NB; ++t) {
-                const u32x4 p0 = xp[(t * 4 + 0) * nchp + ch];
-                const u32x4 p1 = xp[(t * 4 + 1) * nchp + ch];
-                const u32x4 p2 = xp[(t * 4 + 2) * nchp + ch];
-                const u32x4 p3 = xp[(t * 4 + 3) * nchp + ch];
-                const float2 k2 = xk[t * nchp + ch];
-                const float da = dot4(d2, p2, dot4(d0, p0, 0.0f));
-                const float db = dot4(d3, p3, dot4(d1, p1, 0.0f));
-                acc[r][t] = fmaf(sc, (da + db) - k2.y, fmaf(bi, k2.x, acc[r][t]));
+                const float da = dot4(d2, px[t][2], dot4(d0, px[t][0], 0.0f));
+                const float db = dot4(d3, px[t][3], dot4(d1, px[t][1], 0.0f));
+                acc[r][t] = fmaf(sc, (da + db) - k2[t].y, fmaf(bi, k2[t].x, acc[r][t]));
             }
         }
-        if (n < A.nreal && c.j == A.J - 1) finish(c.round);
+        if (c.j == A.J - 1) finish(c.round);
     };
 
     // ---- 4. main loop (loads D items ahead), then the last D items
@@ -285,6 +314,19 @@ __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
         step(ring[d], cc, n + d);
         cc.advance(A.J);
     }
+    if (A.P == 1) return;
+    // ---- 5. K parts: sum the P partials of every round in a fixed order
+    __syncthreads();
+    const uint32_t per_round = A.Q * R * NB, nout = A.rounds * per_round;
+    for (uint32_t i = tid; i < nout; i += nthr) {
+        const uint32_t round = i / per_round, i2 = i - round * per_round;
+        const uint32_t qq = i2 / (R * NB), rt = i2 - qq * (R * NB);
+        const float* pr = part + (size_t)round * (A.P * A.Q) * (R * NB);
+        float v = 0.0f;
+        for (uint32_t pp = 0; pp < A.P; ++pp) v += pr[(qq * A.P + pp) * (R * NB) + rt];
+        const uint32_t gq = round * A.Q + qq, gg = g0 + gq, row = gg * R + rt / NB;
+        if (gq < A.groups_wg && gg < A.ngroups && row < A.M) store(row, rt % NB, v);
+    }
 }
 
 
@@ -298,13 +340,12 @@ uint32_t log2u(uint32_t v) {
 }
 
 // Launch plan: R rows per item, P K-parts, Q row-group lanes, ring depth D.
-// Measured on MI355X (Llama / 70B shapes, batch 1): once running the kernel
-// streams at ~5.9 TB/s and a launch costs ~3.2 us on top, so the plan (1)
-// spreads the row groups over every CU, (2) keeps the per-CU bytes minimal
-// (no idle lanes: Q is cut to the rows a CU has), and (3) uses D = 2 -- deeper
-// rings measured slower at every shape (more rows open at once per CU).
-// Among (R, P) with equal per-CU work, one x read shared by 2 rows and fewer
-// K parts (no LDS reduction) win.
+// Measured on MI355X (Llama / 70B shapes, batch 1), the plan (1) spreads the
+// row groups over every CU, (2) keeps the per-CU bytes minimal (no idle
+// lanes: Q is cut to the rows a CU has), and (3) uses D = 2 -- deeper rings
+// measured slower at every shape. Among (R, P) with equal per-CU work, one x
+// read shared by 2 rows and a single K part win (4096 x 14336: P = 1 7.7 us,
+// P = 7 9.1 us).
 bool make_vplan(uint32_t M, uint32_t K, uint32_t ntok, Int4Cfg cfg, VPlan& out) {
     const uint32_t nch = K >> 5, nstep = (nch + 63) / 64, nchp = nstep * 64, cu = cu_count();
     if (cfg.unroll != 0 && cfg.unroll != 2 && cfg.unroll != 4 && cfg.unroll != 8) return false;
@@ -325,13 +366,15 @@ bool make_vplan(uint32_t M, uint32_t K, uint32_t ntok, Int4Cfg cfg, VPlan& out) 
             const uint32_t nwg = (ngroups + groups_wg - 1) / groups_wg;
             const uint32_t nreal = rounds * J;
             const uint32_t nsteps = (nreal + D - 1) / D * D;
-            const size_t lds = vlds_x(ntok, nchp) + (P > 1 ? (size_t)2 * waves * R * ntok * 4 : 0);
+            const size_t lds = vlds_x(ntok, nchp) + (P > 1 ? (size_t)rounds * waves * R * ntok * 4 : 0);
             if (lds > kLdsMax) continue;
             // per-CU KiB (padding included) plus a latency term for short
-            // waves: fewer than 8 waves or fewer than 2 items leave HBM idle
+            // waves: fewer than 8 waves or fewer than 2 items leave HBM idle.
             double cost = (double)nsteps * waves * R;
             if (waves < 8) cost *= 1.0 + 0.1 * (8 - waves);
-            if (P > 1) cost *= 1.02;
+            // K parts: a wave finishes (reduces) its rows once per item
+            // instead of once per row -- measured 4-17% slower per part count
+            if (P > 1) cost *= 1.0 + 0.05 * P;
             if (R == 2) cost *= 0.98;
             if (!found || cost < best) {
                 found = true;

@@ -121,6 +121,15 @@ def test_forced_launch_shapes_agree(gpu, K, parts, depth, M, batch):
     check(got, ref_int4(p), f"P={parts} D={depth} K={K} M={M} b={batch}")
 
 
+@pytest.mark.parametrize("parts,depth,batch", [(2, 2, 1), (2, 4, 2), (4, 2, 1)])
+def test_forced_kparts_many_rounds(gpu, parts, depth, batch):
+    """K parts over several rounds of row groups per workgroup: every
+    round's partial sums wait in LDS until the one reduction at the end."""
+    p = gen.int4_problem(9000, 8192, 64, batch=batch, seed=5 + parts + depth)
+    got = run_int4(p, gpu, path=kq.PATH_VALU, rows=parts, unroll=depth)
+    check(got, ref_int4(p), f"P={parts} D={depth} M=9000 b={batch}")
+
+
 # (K parts P, 10 * tiles per wave T + ring depth 2)
 MFMA_PLANS = [(16, 12), (1, 12), (8, 22), (2, 22), (4, 42), (8, 42), (1, 42), (4, 2)]
 
