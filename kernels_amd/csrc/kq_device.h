@@ -130,6 +130,22 @@ struct DequantConsts {
     }
 };
 
+// The four fp16-pair operands of one packed word: (1024+n0, 1024+n4),
+// (64+n1, 64+n5), (1024+n2, 1024+n6), (64+n3, 64+n7).
+__device__ __forceinline__ u32x4 dq4(uint32_t w, const DequantConsts& k) {
+    const uint32_t w8 = w >> 8;
+    return u32x4{and_or(w, k.lo, k.e1024), and_or(w, k.hi, k.e64), and_or(w8, k.lo, k.e1024),
+                 and_or(w8, k.hi, k.e64)};
+}
+
+// Dot of four dequantised pairs with their permuted activation pairs.
+__device__ __forceinline__ float dot4(u32x4 d, u32x4 p, float acc) {
+    acc = dot2(d.x, p.x, acc);
+    acc = dot2(d.y, p.y, acc);
+    acc = dot2(d.z, p.z, acc);
+    return dot2(d.w, p.w, acc);
+}
+
 // Dot of one packed word (8 nibbles) with its permuted activation pairs.
 __device__ __forceinline__ float qdot8(uint32_t w, u32x4 p, float acc, const DequantConsts& k) {
     const uint32_t w8 = w >> 8;

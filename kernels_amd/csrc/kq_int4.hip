@@ -68,20 +68,6 @@ struct VSlot<R, false> {
     uint16_t s[R], b[R];  // widened at use: a widening next to the load would wait for it
 };
 
-// The four fp16-pair operands of one packed word (see kq_device.h).
-__device__ __forceinline__ u32x4 dq4(uint32_t w, const DequantConsts& k) {
-    const uint32_t w8 = w >> 8;
-    return u32x4{and_or(w, k.lo, k.e1024), and_or(w, k.hi, k.e64), and_or(w8, k.lo, k.e1024),
-                 and_or(w8, k.hi, k.e64)};
-}
-
-__device__ __forceinline__ float dot4(u32x4 d, u32x4 p, float acc) {
-    acc = dot2(d.x, p.x, acc);
-    acc = dot2(d.y, p.y, acc);
-    acc = dot2(d.z, p.z, acc);
-    return dot2(d.w, p.w, acc);
-}
-
 template <bool BF>
 __device__ __forceinline__ float mval(uint32_t v) {
     if constexpr (BF) return bf2f((uint16_t)v);

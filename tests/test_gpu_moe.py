@@ -106,7 +106,7 @@ def _pool_desc(n):
     return d
 
 
-@pytest.mark.parametrize("batch", [1, 8])
+@pytest.mark.parametrize("batch", [1, 2, 5, 8, 16])
 def test_gate_up_and_down_vs_oracle(gpu, pool16, batch):
     host, pool = pool16
     d = _pool_desc(16)
