@@ -8,17 +8,22 @@
 //   * a wave instruction reads 1 KiB of indices of one row (lane l: the
 //     16-byte chunk 64*step + l = 16 indices = 32 weights);
 //   * the workgroup stages x once in LDS as its natural fp16 pairs (index i
-//     meets dword i of x) in [token][word%4][chunk] layout (conflict-free
-//     ds_read_b128; chunks past K zero-filled), and the codebook blocks of its
-//     rows (256 x half2 = 1 KiB each);
+//     meets dword i of x), one 4 KiB block per (1 KiB step, token) with the
+//     64 lanes' 16-byte pieces of word jw in plane jw (conflict-free
+//     ds_read_b128 at immediate offsets; chunks past K zero-filled), and the
+//     codebook blocks of its rows (256 x half2 = 1 KiB each);
 //   * each index byte addresses one half2 codeword in LDS (ds_read_b32),
 //     dotted with its x pair by v_dot2_f32_f16 (fp32 accumulation); the
 //     lookups are shared by every token of the pass; the scale applies once
 //     per 32-weight chunk (scale_group % 32 == 0) or once per row;
 //   * a workgroup of P*Q waves owns contiguous row groups (R rows); wave (p, q)
 //     takes K-part p of row groups q, q+Q, ...; items stream through a 2-deep
-//     ring of register slots with unconditional clamped loads, the scale kept
-//     as loaded until its use (so a wave waits for one slot at a time).
+//     ring of register slots with unconditional loads, the scale kept as
+//     loaded until its use (so a wave waits for one slot at a time);
+//   * indices and scales come with buffer loads on descriptors based at the
+//     workgroup's first row (row and step offsets scalar; lanes past a
+//     partial last step load out of range: zeros, no traffic); K parts meet
+//     in LDS once per launch.
 #include "kq_device.h"
 #include "kq_internal.h"
 
@@ -27,7 +32,6 @@ namespace kq {
 namespace {
 
 constexpr int kMaxWaves = 16;
-constexpr uint32_t kMaxNB = 4;  // tokens per pass
 constexpr size_t kLdsMax = 160 * 1024;
 
 struct QArgs {
@@ -41,6 +45,8 @@ struct QArgs {
                                            // scales per row, chunk -> scale shift (31: per row)
     uint32_t P, Q, J, groups_wg, ngroups, rounds, nreal, nsteps;
     uint32_t cb_first_div;  // rows of a workgroup span at most this many codebooks
+    uint32_t rpc_shift;     // log2(rows per codebook) if a power of 2; 31: one codebook
+                            // for all rows; 32: divide
 };
 
 struct QPlan {
@@ -79,47 +85,48 @@ __device__ __forceinline__ float vq_word(uint32_t word, u32x4 xv, const uint32_t
     return dot2(cbr[word >> 24], xv.w, acc);
 }
 
+// x in LDS: per (step s, token t) one 4096-byte block of four planes (plane
+// jw = word jw of each of the 64 lanes' chunks, 16 B per lane) at
+// (s * NB + t) * kQBlk: a lane's reads of an item are one base VGPR plus
+// immediate offsets.
+constexpr uint32_t kQBlk = 4096;
+constexpr int kQXr = 8;  // x words a thread stages per pass (one pass up to 8 x threads)
+
 template <int NB, int R, int D>
 __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const uint32_t nch = A.nch, nchp = A.nchp, nw = A.K >> 3;
-    u32x4* xp = reinterpret_cast<u32x4*>(smem);                                  // [NB][4][nchp]
+    constexpr uint32_t kOOB = 0x80000000u;  // past every descriptor's range: loads read zeros
+    const uint32_t nch = A.nch, nchp = A.nchp, nw = A.K >> 3, nstep = nchp >> 6;
     uint32_t* cb = reinterpret_cast<uint32_t*>(smem + qlds_x(NB, nchp));          // [ncb][256]
+    float* part = reinterpret_cast<float*>(cb + (size_t)A.cb_first_div * 256);  // [rounds][waves][R*NB]
 
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
-    const int lane = tid & 63;
-    const uint32_t wave = tid >> 6, p = wave % A.P, q = wave / A.P;
+    const uint32_t lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t p = wave % A.P, q = wave / A.P;
     const uint32_t g0 = blockIdx.x * A.groups_wg;
     const uint32_t last_group = A.ngroups - 1, last_row = A.M - 1;
-    const uint32_t row_first = min(g0 * R, last_row);
-    const uint32_t cb0 = row_first / A.rpc;
-    const u32x4* I4 = reinterpret_cast<const u32x4*>(A.IDX);
+    const uint32_t row0 = g0 * R;
+    const uint32_t cb0 = row0 / A.rpc;
 
-    // ---- 1. x loads first (vmcnt retires in order), then the ring
+    // descriptors based at this workgroup's first row
+    const uint32_t rows_wg = min(A.groups_wg * R, A.M - row0);
+    const uint32_t rowb = A.K >> 1, srowb = A.spr * 2;
+    const rsrc_t rI = make_rsrc(A.IDX + (size_t)row0 * rowb, rows_wg * rowb);
+    const rsrc_t rS = make_rsrc(A.S + (size_t)row0 * A.spr, rows_wg * srowb);
+    const rsrc_t rX = make_rsrc(A.X, NB * A.K * 2);
+
+    // ---- 1. x and codebook loads first (vmcnt retires in order), then the ring
     const uint32_t xtotal = NB * nw;
-    const u32x4* X4 = reinterpret_cast<const u32x4*>(A.X);
-    constexpr int kXr = 2;
-    u32x4 sv[kXr];
-    auto x_load = [&](uint32_t w0) {
+    u32x4 sv[kQXr];
 #pragma unroll
-        for (int r = 0; r < kXr; ++r) {
-            const uint32_t w = w0 + r * nthr + tid;
-            sv[r] = X4[w < xtotal ? w : xtotal - 1];
+    for (int r = 0; r < kQXr; ++r) {
+        if ((uint32_t)r * nthr < xtotal) {  // uniform
+            const uint32_t w = r * nthr + tid;
+            sv[r] = __builtin_amdgcn_raw_buffer_load_b128(rX, w < xtotal ? w * 16 : kOOB, 0, 0);
         }
-    };
-    auto x_store = [&](uint32_t w0) {
-#pragma unroll
-        for (int r = 0; r < kXr; ++r) {
-            const uint32_t w = w0 + r * nthr + tid;
-            if (w < xtotal) {
-                const uint32_t t = w / nw, wi = w - t * nw;
-                xp[(t * 4 + (wi & 3)) * nchp + (wi >> 2)] = sv[r];
-            }
-        }
-    };
-    x_load(0);
-    // codebook blocks of this workgroup's rows (one dword per thread per round;
-    // at most 4 KiB, ahead of the weights like x)
+    }
+    // codebook blocks of this workgroup's rows (at most 4 KiB)
     const uint32_t ncb_total = (A.M + A.rpc - 1) / A.rpc;
     const uint32_t ncb = min(A.cb_first_div, ncb_total - cb0), cbn = ncb * 256;
     const uint32_t* Cw = reinterpret_cast<const uint32_t*>(A.C) + (size_t)cb0 * 256;
@@ -131,19 +138,31 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
+    // lane offsets: full steps, and the last step (out of range past the row)
+    const uint32_t cl = (nstep - 1) * 64 + lane;
+    const uint32_t vi_full = lane * 16, vi_last = cl < nch ? lane * 16 : kOOB;
+    const bool per_row = A.cshift == 31;
+    const uint32_t vs_full = per_row ? 0u : A.cshift <= 6 ? (lane >> A.cshift) * 2 : 0u;
+    const uint32_t vs_last = cl < nch ? vs_full : kOOB;
+    auto scale_step = [&](uint32_t s) __attribute__((always_inline)) {  // scale index of step s
+        return per_row ? 0u : A.cshift <= 6 ? s * (64u >> A.cshift) : s >> (A.cshift - 6);
+    };
     QSlot<R> ring[D];
-    auto issue = [&](QSlot<R>& e, Cursor c) {
+    auto issue = [&](QSlot<R>& e, Cursor c) __attribute__((always_inline)) {
         if (c.round >= A.rounds) {  // padding item: re-read the last real one
             c.round = A.rounds - 1;
             c.j = A.J - 1;
         }
         const uint32_t grp = min(g0 + c.round * A.Q + q, last_group);
-        const uint32_t ch = min((p * A.J + c.j) * 64 + lane, nch - 1);
+        const uint32_t s = __builtin_amdgcn_readfirstlane(p * A.J + c.j);
+        const bool last = s == nstep - 1;
+        const uint32_t vi = last ? vi_last : vi_full, vs = last ? vs_last : vs_full;
+        const uint32_t so = scale_step(s) * 2;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t row = min(grp * R + r, last_row);
-            e.idx[r] = ldg_nt(I4 + (size_t)row * nch + ch);
-            e.sc[r] = A.S[(size_t)row * A.spr + (A.cshift == 31 ? 0 : ch >> A.cshift)];
+            const uint32_t rr = __builtin_amdgcn_readfirstlane(min(grp * R + r, last_row) - row0);
+            e.idx[r] = __builtin_amdgcn_raw_buffer_load_b128(rI, vi, rr * rowb + s * 1024, kNT);
+            e.sc[r] = __builtin_amdgcn_raw_buffer_load_b16(rS, vs, rr * srowb + so, 0);
         }
     };
     Cursor ci{0, 0};
@@ -154,16 +173,33 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- 2. finish staging: x, zero padding, codebooks
-    x_store(0);
-    for (uint32_t w0 = kXr * nthr; w0 < xtotal; w0 += kXr * nthr) {
-        x_load(w0);
-        x_store(w0);
+    // ---- 2. finish staging: x (as loaded: index i meets dword i), zero
+    // padding, codebooks
+#pragma unroll
+    for (int r = 0; r < kQXr; ++r) {
+        if ((uint32_t)r * nthr < xtotal) {  // uniform
+            const uint32_t w = r * nthr + tid;
+            if (w < xtotal) {
+                const uint32_t t = w / nw, wi = w - t * nw, ch = wi >> 2;
+                *reinterpret_cast<u32x4*>(smem + ((ch >> 6) * NB + t) * kQBlk + (wi & 3) * 1024 +
+                                          (ch & 63) * 16) = sv[r];
+            }
+        }
+    }
+    for (uint32_t w0 = kQXr * nthr; w0 < xtotal; w0 += nthr) {  // only past 8 words per thread
+        const uint32_t w = w0 + tid;
+        if (w < xtotal) {
+            const uint32_t t = w / nw, wi = w - t * nw, ch = wi >> 2;
+            *reinterpret_cast<u32x4*>(smem + ((ch >> 6) * NB + t) * kQBlk + (wi & 3) * 1024 +
+                                      (ch & 63) * 16) = reinterpret_cast<const u32x4*>(A.X)[w];
+        }
     }
     const uint32_t npad = nchp - nch;
     for (uint32_t i = tid; i < NB * 4 * npad; i += nthr) {
-        const uint32_t tj = i / npad;
-        xp[tj * nchp + nch + (i - tj * npad)] = u32x4{0, 0, 0, 0};
+        const uint32_t t = i / (4 * npad), rem = i - t * 4 * npad, jw = rem / npad;
+        const uint32_t ch = nch + (rem - jw * npad);
+        *reinterpret_cast<u32x4*>(smem + ((ch >> 6) * NB + t) * kQBlk + jw * 1024 + (ch & 63) * 16) =
+            u32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -179,26 +215,29 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
 #pragma unroll
         for (int t = 0; t < NB; ++t) acc[r][t] = 0.0f;
 
-    auto finish = [&](uint32_t round) {
-        const uint32_t gl = round * A.Q + q, grp = g0 + gl;
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int t = 0; t < NB; ++t) {
-                const float v = wave_sum(acc[r][t]);
-                acc[r][t] = 0.0f;
-                const uint32_t row = grp * R + r;
-                if (lane == 0 && gl < A.groups_wg && grp < A.ngroups && row < A.M) {
-                    const size_t o = (size_t)t * A.M + row;
-                    if (A.y_f32) reinterpret_cast<float*>(A.Y)[o] = v;
-                    else reinterpret_cast<uint16_t*>(A.Y)[o] = f2h(v);
-                }
-            }
+    auto store = [&](uint32_t row, uint32_t t, float v) __attribute__((always_inline)) {
+        const size_t o = (size_t)t * A.M + row;
+        if (A.y_f32) reinterpret_cast<float*>(A.Y)[o] = v;
+        else reinterpret_cast<uint16_t*>(A.Y)[o] = f2h(v);
     };
-    // P parts of a row meet in LDS (after the x stage, which stays live)
-    float* part = reinterpret_cast<float*>(cb + (size_t)A.cb_first_div * 256);  // [2][waves][R*NB]
-    auto finish_split = [&](uint32_t round) {
-        float* pw = part + ((size_t)(round & 1) * (A.P * A.Q) + wave) * (R * NB);
+    auto finish = [&](uint32_t round) __attribute__((always_inline)) {
+        const uint32_t gl = round * A.Q + q, grp = g0 + gl;
+        if (A.P == 1) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int t = 0; t < NB; ++t) {
+                    const float v = wave_sum(acc[r][t]);
+                    acc[r][t] = 0.0f;
+                    const uint32_t row = grp * R + r;
+                    if (lane == 0 && gl < A.groups_wg && grp < A.ngroups && row < A.M)
+                        store(row, t, v);
+                }
+            return;
+        }
+        // K parts: the round's partial sums wait in LDS for one reduction
+        // after the stream
+        float* pw = part + ((size_t)round * (A.P * A.Q) + wave) * (R * NB);
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -207,32 +246,22 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
                 acc[r][t] = 0.0f;
                 if (lane == 0) pw[r * NB + t] = v;
             }
-        __syncthreads();
-        const float* pr = part + (size_t)(round & 1) * (A.P * A.Q) * (R * NB);
-        for (uint32_t i = tid; i < A.Q * R * NB; i += nthr) {
-            const uint32_t qq = i / (R * NB), rt = i - qq * (R * NB);
-            float v = 0.0f;
-            for (uint32_t pp = 0; pp < A.P; ++pp) v += pr[(qq * A.P + pp) * (R * NB) + rt];
-            const uint32_t gq = round * A.Q + qq, gg = g0 + gq, row = gg * R + rt / NB;
-            if (gq < A.groups_wg && gg < A.ngroups && row < A.M) {
-                const size_t o = (size_t)(rt % NB) * A.M + row;
-                if (A.y_f32) reinterpret_cast<float*>(A.Y)[o] = v;
-                else reinterpret_cast<uint16_t*>(A.Y)[o] = f2h(v);
-            }
-        }
     };
-    auto step = [&](const QSlot<R>& e, Cursor c, uint32_t n) {
-        const uint32_t ch = (p * A.J + c.j) * 64 + lane;
-        const uint32_t grp = min(g0 + min(c.round, A.rounds - 1) * A.Q + q, last_group);
+    const uint32_t rshift = A.rpc_shift;  // 31: every row uses the first block
+    auto step = [&](const QSlot<R>& e, Cursor c, uint32_t n) __attribute__((always_inline)) {
+        if (n >= A.nreal) return;  // padding to the ring depth (uniform)
+        const unsigned char* bx = smem + lane * 16 + (p * A.J + c.j) * (NB * kQBlk);
+        const uint32_t grp = min(g0 + c.round * A.Q + q, last_group);
         u32x4 xv[NB][4];
 #pragma unroll
         for (int t = 0; t < NB; ++t)
 #pragma unroll
-            for (int w = 0; w < 4; ++w) xv[t][w] = xp[(t * 4 + w) * nchp + ch];
+            for (int w = 0; w < 4; ++w) xv[t][w] = *reinterpret_cast<const u32x4*>(bx + t * kQBlk + w * 1024);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t row = min(grp * R + r, last_row);
-            const uint32_t blk = row / A.rpc - cb0;  // uniform
+            const uint32_t blk =
+                rshift == 31 ? 0u : (rshift < 31 ? row >> rshift : row / A.rpc) - cb0;  // uniform
             u32x4 iv = e.idx[r];
             uint32_t sr = e.sc[r];
             asm volatile("" : "+v"(iv), "+v"(sr));  // use the loaded values here, not earlier
@@ -247,10 +276,7 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
                 acc[r][t] = fmaf(sc, da + db, acc[r][t]);
             }
         }
-        if (n < A.nreal && c.j == A.J - 1) {
-            if (A.P == 1) finish(c.round);
-            else finish_split(c.round);
-        }
+        if (c.j == A.J - 1) finish(c.round);
     };
 
     Cursor cc{0, 0};
@@ -268,6 +294,19 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
     for (int d = 0; d < D; ++d) {
         step(ring[d], cc, n + d);
         cc.advance(A.J);
+    }
+    if (A.P == 1) return;
+    // ---- 3. K parts: sum the P partials of every round in a fixed order
+    __syncthreads();
+    const uint32_t per_round = A.Q * R * NB, nout = A.rounds * per_round;
+    for (uint32_t i = tid; i < nout; i += nthr) {
+        const uint32_t round = i / per_round, i2 = i - round * per_round;
+        const uint32_t qq = i2 / (R * NB), rt = i2 - qq * (R * NB);
+        const float* pr = part + (size_t)round * (A.P * A.Q) * (R * NB);
+        float v = 0.0f;
+        for (uint32_t pp = 0; pp < A.P; ++pp) v += pr[(qq * A.P + pp) * (R * NB) + rt];
+        const uint32_t gq = round * A.Q + qq, gg = g0 + gq, row = gg * R + rt / NB;
+        if (gq < A.groups_wg && gg < A.ngroups && row < A.M) store(row, rt % NB, v);
     }
 }
 
@@ -295,12 +334,14 @@ bool make_qplan(uint32_t M, uint32_t K, uint32_t ntok, uint32_t rpc, QPlan& out)
             const uint32_t ncb = (rows_wg - 1) / rpc + 2 < (M + rpc - 1) / rpc
                                      ? (rows_wg - 1) / rpc + 2
                                      : (M + rpc - 1) / rpc;
-            const size_t fixed = qlds_x(ntok, nchp) + (P > 1 ? (size_t)2 * waves * R * ntok * 4 : 0);
+            const size_t fixed =
+                qlds_x(ntok, nchp) + (P > 1 ? (size_t)rounds * waves * R * ntok * 4 : 0);
             const size_t lds = fixed + (size_t)ncb * 1024;
             if (lds > kLdsMax) continue;
             double cost = (double)nsteps * waves * R;
             if (waves < 8) cost *= 1.0 + 0.1 * (8 - waves);
-            if (P > 1) cost *= 1.02;
+            // K parts finish (reduce) once per item instead of once per row
+            if (P > 1) cost *= 1.0 + 0.05 * P;
             if (R == 2) cost *= 0.98;
             if (!found || cost < best) {
                 found = true;
@@ -375,6 +416,11 @@ hipError_t launch_vq(const uint8_t* IDX, const uint16_t* C, const uint16_t* S, c
         a.nreal = pl.nreal;
         a.nsteps = pl.nsteps;
         a.cb_first_div = pl.ncb;
+        a.rpc_shift = rows_per_cb >= M ? 31u : 32u;
+        if (rows_per_cb < M && (rows_per_cb & (rows_per_cb - 1)) == 0) {
+            a.rpc_shift = 0;
+            while ((1u << a.rpc_shift) < rows_per_cb) ++a.rpc_shift;
+        }
         hipError_t e;
         if (nb == 4) e = qgo_nb<4>(a, pl, s);
         else if (nb == 2) e = qgo_nb<2>(a, pl, s);

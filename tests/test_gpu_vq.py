@@ -65,7 +65,9 @@ def test_index_readback_exact(gpu):
                                               (1000, 2880, 7, 32, 1), (513, 4096, 256, 4096, 3),
                                               (100, 8192, 100, 128, 4),
                                               # short and long: split K over waves + LDS sum
-                                              (64, 28672, 64, 32, 1), (130, 14336, 256, 14336, 2)])
+                                              (64, 28672, 64, 32, 1), (130, 14336, 256, 14336, 2),
+                                              # scale groups longer than a 2048-weight step
+                                              (200, 8192, 256, 4096, 1), (96, 16384, 64, 8192, 2)])
 def test_edge_shapes(gpu, M, K, rpc, sg, batch):
     p = gen.vq_problem(M, K, rows_per_cb=rpc, scale_group=sg, batch=batch, seed=M + sg)
     assert_close(run_vq(p, gpu), ref_vq(p), what=f"vq M={M} K={K} rpc={rpc} sg={sg} b={batch}")
