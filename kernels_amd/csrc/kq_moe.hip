@@ -150,6 +150,9 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
 // index, NaN and -inf are never selectable, a pass with nothing selectable
 // picks expert 0 -- then softmax over the chosen logits. Up to 256 experts
 // (4 per lane); the passes are DPP reductions of cand_key, no LDS traffic.
+// COHERENT: the logits come from other workgroups of the same launch
+// (device-coherent loads); otherwise from an earlier launch (plain loads).
+template <bool COHERENT>
 __device__ void topk_wave(const float* L, uint32_t NE, uint32_t TK,
                           uint32_t* idx_out, float* wgt_out) {
     const uint32_t lane = threadIdx.x & 63;
@@ -158,7 +161,10 @@ __device__ void topk_wave(const float* L, uint32_t NE, uint32_t TK,
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t ei = lane + 64 * q;
-        v[q] = __hip_atomic_load(L + min(ei, NE - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (COHERENT)
+            v[q] = __hip_atomic_load(L + min(ei, NE - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            v[q] = L[min(ei, NE - 1)];
         key[q] = ei < NE ? cand_key(v[q], ei) : 0;  // past NE: never the best (index ~ei > NE)
     }
     float chosen[kMaxTopK];
@@ -248,7 +254,7 @@ __device__ void build_plan(const uint32_t* s_idx, uint32_t nslots, uint32_t NE, 
 // elements 8(l + 64i), i < IT (IT * 512 >= hidden); every router and x load
 // is issued before the first multiply (addresses clamped, results past the
 // row masked), so a wave pays one memory round trip.
-template <bool RF32, bool XF32, int IT>
+template <bool RF32, bool XF32, int IT, bool TAIL>
 __global__ __launch_bounds__(kRtThreads) void moe_router_k(
     const void* __restrict__ R, const void* __restrict__ X, uint32_t batch, uint32_t NE,
     uint32_t HID, uint32_t TK, uint16_t* __restrict__ xh, float* lg, uint32_t* cnt,
@@ -297,6 +303,8 @@ __global__ __launch_bounds__(kRtThreads) void moe_router_k(
             __hip_atomic_store(lg + (size_t)(t0 + t) * NE + e, v, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     }
+    // without the tail, the next launch runs the top-k from the logits
+    if constexpr (!TAIL) return;
     // this workgroup's logits have reached the device-coherent level before
     // it is counted; the last one counted sees every logit
     __builtin_amdgcn_s_waitcnt(0);
@@ -313,7 +321,7 @@ __global__ __launch_bounds__(kRtThreads) void moe_router_k(
     __shared__ uint32_t bits[8];
     __shared__ Plan ps;
     for (uint32_t t = wave; t < batch; t += kRtThreads / 64)
-        topk_wave(lg + (size_t)t * NE, NE, TK, s_idx + t * TK, s_wgt + t * TK);
+        topk_wave<true>(lg + (size_t)t * NE, NE, TK, s_idx + t * TK, s_wgt + t * TK);
     __syncthreads();
     const uint32_t nslots = batch * TK;
     if (tid < nslots) {
@@ -454,6 +462,62 @@ __device__ void get_plan(const Plan* plan_g, const uint32_t* idx, const float* w
     } else {
         __syncthreads();
         build_plan(s_idx, nslots, NE, ps, bits);
+    }
+}
+
+// The router's tail run by a workgroup of the next launch: top-k + softmax of
+// every token from the logits lg (one wave per token), then the plan;
+// workgroup 0 publishes idx, wgt and the plan for the down launch.
+__device__ void plan_from_logits(const float* lg, uint32_t batch, uint32_t NE, uint32_t TK,
+                                 Plan& ps, uint32_t* s_idx, float* s_wgt, uint32_t* bits,
+                                 uint32_t* idx_out, float* wgt_out, Plan* plan_out) {
+    const uint32_t tid = threadIdx.x;
+    for (uint32_t t = tid >> 6; t < batch; t += blockDim.x >> 6)
+        topk_wave<false>(lg + (size_t)t * NE, NE, TK, s_idx + t * TK, s_wgt + t * TK);
+    __syncthreads();
+    const uint32_t nslots = batch * TK;
+    if (nslots <= 64) {
+        // one wave: lane s holds slot s's expert; the distinct experts in
+        // ascending order, each with the mask of its slots (as build_plan)
+        if (tid < 64) {
+            const uint32_t e = tid < nslots ? min(s_idx[tid], NE - 1) : 0xFFFFFFFFu;
+            uint64_t m = 0;
+            uint32_t rank = 0;
+            bool first = true;
+            for (uint32_t s2 = 0; s2 < nslots; ++s2) {
+                const uint32_t e2 = __builtin_amdgcn_readlane(e, s2);
+                uint32_t f2 = 1;  // slot s2 is its expert's first slot
+                for (uint32_t s3 = 0; s3 < s2; ++s3)
+                    f2 &= __builtin_amdgcn_readlane(e, s3) != e2 ? 1u : 0u;
+                if (e2 == e) {
+                    m |= 1ull << s2;
+                    if (s2 < tid) first = false;
+                }
+                if (f2 && e2 < e) ++rank;
+            }
+            if (tid < nslots && first) {
+                ps.expert[rank] = e;
+                ps.mask[rank][0] = m;
+                ps.mask[rank][1] = 0;
+            }
+            const uint64_t firsts = __ballot(tid < nslots && first);
+            if (tid == 0) ps.n = __popcll(firsts);
+        }
+        __syncthreads();
+    } else {
+        build_plan(s_idx, nslots, NE, ps, bits);
+    }
+    if (blockIdx.x == 0) {
+        if (tid < nslots) {
+            idx_out[tid] = s_idx[tid];
+            wgt_out[tid] = s_wgt[tid];
+        }
+        if (tid == 0) plan_out->n = ps.n;
+        for (uint32_t u = tid; u < ps.n; u += blockDim.x) {
+            plan_out->expert[u] = ps.expert[u];
+            plan_out->mask[u][0] = ps.mask[u][0];
+            plan_out->mask[u][1] = ps.mask[u][1];
+        }
     }
 }
 
@@ -804,11 +868,14 @@ __device__ __forceinline__ float swiglu(float g, float u) {
 // w takes a contiguous range, wave q every kStWaves-th item of it. Half 0
 // reads gate row i, half 1 up row i. XREG (one token): the token's
 // activation chunks stay in registers for the whole stream.
-template <int J, bool FROM_PLAN, bool XREG>
+// SRC: 0 plan from idx, 1 plan from the router, 2 top-k from the router's
+// logits (lg) here, publishing idx / wgt / plan (workgroup 0).
+template <int J, int SRC, bool XREG>
 __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     const uint8_t* __restrict__ pool, kq_moe_desc d, const uint32_t* __restrict__ idx,
     const Plan* __restrict__ plan_g, const uint16_t* __restrict__ xh, uint16_t* __restrict__ H,
-    uint32_t batch) {
+    uint32_t batch, const float* __restrict__ lg, uint32_t* __restrict__ idx_out,
+    float* __restrict__ wgt_out, Plan* __restrict__ plan_out) {
     extern __shared__ __align__(16) unsigned char act[];
     __shared__ Plan ps;
     __shared__ uint32_t s_idx[kMaxSlots];
@@ -820,7 +887,11 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
 
     StStage st;
     st_stage_load(st, xh, batch, K);
-    get_plan<FROM_PLAN>(plan_g, idx, nullptr, batch * TK, d.n_experts, ps, s_idx, s_wgt, bits);
+    if constexpr (SRC == 2)
+        plan_from_logits(lg, batch, d.n_experts, TK, ps, s_idx, s_wgt, bits, idx_out, wgt_out,
+                         plan_out);
+    else
+        get_plan<SRC == 1>(plan_g, idx, nullptr, batch * TK, d.n_experts, ps, s_idx, s_wgt, bits);
     const uint32_t nexp = ps.n, N = nexp * IN;
     const uint32_t per = (N + gridDim.x - 1) / gridDim.x, k0 = blockIdx.x * per;
     const uint32_t cnt = k0 < N ? min(per, N - k0) : 0;
@@ -1012,7 +1083,7 @@ __global__ void fill_zero_k(uint32_t* p, size_t n) {
 
 uint32_t chunks_j(uint32_t K) { return ((K >> 5) + 31) / 32; }
 
-template <int IT>
+template <int IT, bool TAIL>
 hipError_t launch_router_it(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
                             const kq_moe_desc& d, uint16_t* xh, const WsLayout& L, uint8_t* ws,
                             uint32_t* idx, float* wgt, hipStream_t s) {
@@ -1021,7 +1092,7 @@ hipError_t launch_router_it(const void* R, bool r_f32, const void* X, bool x_f32
     uint32_t* cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
     Plan* plan = reinterpret_cast<Plan*>(ws + L.plan);
 #define KQ_RT(RF, XF)                                                                     \
-    moe_router_k<RF, XF, IT><<<grid, kRtThreads, 0, s>>>(R, X, batch, d.n_experts, d.hidden, \
+    moe_router_k<RF, XF, IT, TAIL><<<grid, kRtThreads, 0, s>>>(R, X, batch, d.n_experts, d.hidden, \
                                                          d.top_k, xh, lg, cnt, idx, wgt, plan)
     if (r_f32 && x_f32) KQ_RT(true, true);
     else if (r_f32) KQ_RT(true, false);
@@ -1031,16 +1102,24 @@ hipError_t launch_router_it(const void* R, bool r_f32, const void* X, bool x_f32
     return hipGetLastError();
 }
 
-hipError_t launch_router(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
-                         const kq_moe_desc& d, uint16_t* xh, void* ws, uint32_t* idx, float* wgt,
-                         hipStream_t s) {
+template <bool TAIL>
+hipError_t launch_router_t(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
+                           const kq_moe_desc& d, uint16_t* xh, void* ws, uint32_t* idx, float* wgt,
+                           hipStream_t s) {
     const WsLayout L = ws_layout(d, batch);
     uint8_t* w = reinterpret_cast<uint8_t*>(ws);
     const uint32_t it = (d.hidden + 511) / 512;  // hidden <= 4096 (validated)
-    if (it <= 2) return launch_router_it<2>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
-    if (it <= 4) return launch_router_it<4>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
-    if (it <= 6) return launch_router_it<6>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
-    return launch_router_it<8>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
+    if (it <= 2) return launch_router_it<2, TAIL>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
+    if (it <= 4) return launch_router_it<4, TAIL>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
+    if (it <= 6) return launch_router_it<6, TAIL>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
+    return launch_router_it<8, TAIL>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
+}
+
+// Router with its tail: logits, then (last workgroup) top-k, idx/wgt and plan.
+hipError_t launch_router(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
+                         const kq_moe_desc& d, uint16_t* xh, void* ws, uint32_t* idx, float* wgt,
+                         hipStream_t s) {
+    return launch_router_t<true>(R, r_f32, X, x_f32, batch, d, xh, ws, idx, wgt, s);
 }
 
 template <int J, bool FP>
@@ -1069,23 +1148,28 @@ bool st_ok(const kq_moe_desc& d, uint32_t nvec, uint32_t K, size_t extra) {
            st_act_bytes(nvec, K) + extra + kStStatic <= kLdsMax;
 }
 
-template <int J, bool FP>
+// Top-k in the gate/up launch (SRC 2): the logits, and where idx / wgt /
+// plan go.
+struct GuTopk {
+    const float* lg;
+    uint32_t* idx;
+    float* wgt;
+    Plan* plan;
+};
+
+template <int J, int SRC>
 hipError_t go_gu_st(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
                     const Plan* plan, const uint16_t* xh, uint16_t* H, uint32_t batch,
-                    hipStream_t s) {
+                    GuTopk tk, hipStream_t s) {
     const size_t lds = st_act_bytes(batch, d.hidden);
-    if (batch == 1) {
-        auto kern = moe_gu_stream_k<J, FP, true>;
+    auto run = [&](auto kern) {
         const hipError_t e = st_lds(kern, lds);
         if (e != hipSuccess) return e;
-        kern<<<cu_count(), 64 * kStWaves, lds, s>>>(pool, d, idx, plan, xh, H, batch);
-    } else {
-        auto kern = moe_gu_stream_k<J, FP, false>;
-        const hipError_t e = st_lds(kern, lds);
-        if (e != hipSuccess) return e;
-        kern<<<cu_count(), 64 * kStWaves, lds, s>>>(pool, d, idx, plan, xh, H, batch);
-    }
-    return hipGetLastError();
+        kern<<<cu_count(), 64 * kStWaves, lds, s>>>(pool, d, idx, plan, xh, H, batch, tk.lg,
+                                                     tk.idx, tk.wgt, tk.plan);
+        return hipGetLastError();
+    };
+    return batch == 1 ? run(moe_gu_stream_k<J, SRC, true>) : run(moe_gu_stream_k<J, SRC, false>);
 }
 
 template <int J, bool FP>
@@ -1102,21 +1186,31 @@ hipError_t go_dn_st(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* i
     return hipGetLastError();
 }
 
+// Streaming gate/up: measured (gpt-oss shapes) 12.0 us vs per-tile 13.9 us
+// at one token; at 8 tokens the per-tile kernel wins (69.5 vs 78.5 us).
+bool gu_streams(const kq_moe_desc& d, uint32_t batch) {
+    return batch <= 2 && st_ok(d, batch, d.hidden, 0);
+}
+
+template <int SRC>
+hipError_t launch_gu_st(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
+                        const Plan* plan, const uint16_t* xh, uint16_t* H, uint32_t batch,
+                        GuTopk tk, hipStream_t s) {
+    switch (chunks_j(d.hidden)) {
+        case 1: return go_gu_st<1, SRC>(pool, d, idx, plan, xh, H, batch, tk, s);
+        case 2: return go_gu_st<2, SRC>(pool, d, idx, plan, xh, H, batch, tk, s);
+        case 3: return go_gu_st<3, SRC>(pool, d, idx, plan, xh, H, batch, tk, s);
+        case 4: return go_gu_st<4, SRC>(pool, d, idx, plan, xh, H, batch, tk, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 template <bool FP>
 hipError_t launch_gu(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
                      const Plan* plan, const uint16_t* xh, uint16_t* H, uint32_t batch,
                      hipStream_t s) {
-    // measured (gpt-oss shapes): streaming 12.0 us vs per-tile 13.9 us at one
-    // token; at 8 tokens the per-tile kernel wins (69.5 vs 78.5 us)
-    if (batch <= 2 && st_ok(d, batch, d.hidden, 0)) {
-        switch (chunks_j(d.hidden)) {
-            case 1: return go_gu_st<1, FP>(pool, d, idx, plan, xh, H, batch, s);
-            case 2: return go_gu_st<2, FP>(pool, d, idx, plan, xh, H, batch, s);
-            case 3: return go_gu_st<3, FP>(pool, d, idx, plan, xh, H, batch, s);
-            case 4: return go_gu_st<4, FP>(pool, d, idx, plan, xh, H, batch, s);
-            default: return hipErrorInvalidValue;
-        }
-    }
+    if (gu_streams(d, batch))
+        return launch_gu_st<FP ? 1 : 0>(pool, d, idx, plan, xh, H, batch, GuTopk{}, s);
     switch (chunks_j(d.hidden)) {
         case 1: return go_gu<1, FP>(pool, d, idx, plan, xh, H, batch, s);
         case 2: return go_gu<2, FP>(pool, d, idx, plan, xh, H, batch, s);
@@ -1186,16 +1280,30 @@ hipError_t launch_moe_down(const uint8_t* pool, const kq_moe_desc& d, const uint
     return launch_dn<false>(pool, d, idx, wgt, nullptr, H, Y, y_f32, batch, s);
 }
 
+// The block's three launches. With the streaming gate/up (1-2 tokens) the
+// router's top-k tail moves into the gate/up launch: every gate/up workgroup
+// selects from the logits (cheap, L2-resident) instead of the router's last
+// workgroup doing it after a device-scope hand-off (measured 8.1 -> 3.3 us
+// for the router at one token).
 hipError_t launch_moe_block(const uint8_t* pool, const kq_moe_desc& d, const void* R, bool r_f32,
                             const void* X, bool x_f32, uint32_t batch, uint32_t* idx, float* wgt,
                             uint16_t* xh, uint16_t* H, void* Y, bool y_f32, void* ws,
                             hipStream_t s) {
-    hipError_t e = launch_router(R, r_f32, X, x_f32, batch, d, xh, ws, idx, wgt, s);
-    if (e != hipSuccess) return e;
-    const Plan* plan =
-        reinterpret_cast<const Plan*>(reinterpret_cast<const uint8_t*>(ws) + ws_layout(d, batch).plan);
+    const WsLayout L = ws_layout(d, batch);
+    uint8_t* w = reinterpret_cast<uint8_t*>(ws);
+    Plan* plan = reinterpret_cast<Plan*>(w + L.plan);
     const uint16_t* xin = x_f32 ? xh : reinterpret_cast<const uint16_t*>(X);
-    e = launch_gu<true>(pool, d, idx, plan, xin, H, batch, s);
+    hipError_t e;
+    if (gu_streams(d, batch)) {
+        e = launch_router_t<false>(R, r_f32, X, x_f32, batch, d, xh, ws, idx, wgt, s);
+        if (e != hipSuccess) return e;
+        const GuTopk tk{reinterpret_cast<const float*>(w + L.lg), idx, wgt, plan};
+        e = launch_gu_st<2>(pool, d, idx, plan, xin, H, batch, tk, s);
+    } else {
+        e = launch_router(R, r_f32, X, x_f32, batch, d, xh, ws, idx, wgt, s);
+        if (e != hipSuccess) return e;
+        e = launch_gu<true>(pool, d, idx, plan, xin, H, batch, s);
+    }
     if (e != hipSuccess) return e;
     return launch_dn<true>(pool, d, idx, wgt, plan, H, Y, y_f32, batch, s);
 }
