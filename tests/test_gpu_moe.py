@@ -234,3 +234,57 @@ def test_block_graph_replays(gpu, pool16, batch):
         block()  # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(b.y, ref_y), f"eager after replay {rep}"
+
+
+def _compact_desc(hidden, inter, n_experts, top_k):
+    """A blob layout for other shapes: gate, up, down one after another, each
+    W, S, B, BI (256-byte aligned); returns (kq desc, offsets for gen)."""
+    def al(v):
+        return (v + 255) // 256 * 256
+    # every projection shares the sub-offsets, so size them for the largest
+    rows_cols = [(inter, hidden), (inter, hidden), (hidden, inter)]
+    wmax = max(r * c // 2 for r, c in rows_cols)
+    smax = max(r * (c // 64) * 2 for r, c in rows_cols)
+    bimax = max(r * 2 for r, c in rows_cols)
+    sub = dict(sub_w=0, sub_s=al(wmax), sub_b=al(wmax) + al(smax), sub_bi=al(wmax) + 2 * al(smax))
+    proj = al(sub["sub_bi"] + bimax)
+    off = dict(off_gate=0, off_up=proj, off_down=2 * proj, **sub)
+    d = kq.moe_default_desc()
+    d.hidden, d.inter, d.n_experts, d.top_k = hidden, inter, n_experts, top_k
+    d.blob = 3 * proj
+    for k, v in off.items():
+        setattr(d, k, v)
+    return d, off
+
+
+@pytest.mark.parametrize("hidden,inter,batch", [(1024, 2048, 1), (4096, 512, 2), (2048, 4096, 1),
+                                                (1536, 1024, 3)])
+def test_other_shapes(gpu, hidden, inter, batch):
+    """Descriptors other than gpt-oss's (every chunk count of the streaming
+    kernels, partial chunks, 16 experts, top-3): the block and the
+    standalone projections against the oracle, routing exact."""
+    d, off = _compact_desc(hidden, inter, 16, 3)
+    host = gen.moe_pool(16, seed=hidden + inter, quantize=True, hidden=hidden, inter=inter,
+                        blob=d.blob, off=off)
+    pool = dev(host, gpu)
+    R, X = gen.moe_inputs(16, hidden=hidden, batch=batch, seed=inter + batch)
+    oidx, owgt, lg = oracle.moe_router(R, oracle.F16, X, oracle.F16, batch, odesc(d))
+    assert routing_margin(lg, 3) > 1e-5
+    _, _, Yref = oracle.moe_block(host, odesc(d), R, oracle.F16, X, oracle.F16, batch)
+    b = Block(gpu, d, batch)
+    Rd, Xd = dev(R, gpu).view(torch.float16), dev(X, gpu).view(torch.float16)
+    kq.moe_block(pool, d, Rd, Xd, b.idx, b.wgt, b.H, b.y, b.ws, b.wsb, batch=batch)
+    torch.cuda.synchronize()
+    assert np.array_equal(b.idx.cpu().numpy().astype(np.uint32), oidx)
+    assert np.allclose(b.wgt.cpu().numpy(), owgt, atol=1e-6)
+    assert_close(to_f64(b.y), Yref, what=f"block {hidden}x{inter} b{batch}")
+    # the standalone projections from the same routing
+    kq.moe_gate_up_swiglu(pool, d, b.idx, Xd, b.H, b.ws, b.wsb, batch=batch)
+    torch.cuda.synchronize()
+    Href = oracle.moe_gate_up(host, odesc(d), oidx, X, oracle.F16, batch)
+    assert_close(to_f64(b.H), Href, what=f"h {hidden}x{inter} b{batch}")
+    kq.moe_down_combine(pool, d, b.idx, b.wgt, b.H, b.y, b.ws, b.wsb, batch=batch)
+    torch.cuda.synchronize()
+    Yd = oracle.moe_down(host, odesc(d), oidx, b.wgt.cpu().numpy().astype(np.float64),
+                         host_bits(b.H, np.uint16), batch)
+    assert_close(to_f64(b.y), Yd, atol=1e-4, rtol=1e-4, what=f"down {hidden}x{inter} b{batch}")
