@@ -293,6 +293,23 @@ def bench_moe(torch, kq, dev, args, timer, res, n_layers=36):
                                     gbs=round(b / (ms * 1e-3) / 1e9, 1),
                                     frac=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
         del g
+        if batch == 1:
+            # the same layers one operation per launch (encodeUnfused,
+            # moe-fused/src/main.mm:208-284), also replayed from a graph
+            nuw = kq.moe_unfused_workspace_size(d)
+            uws = torch.empty(nuw, dtype=torch.uint8, device=dev)
+            nl = [0]
+
+            def ustep():
+                for l in range(n_layers):
+                    nl[0] = kq.moe_block_unfused(pools[l], d, Rs[l], xs[l], idx[l], wgt[l], H, Y,
+                                                 uws, nuw)
+            g = graph_of(torch, ustep)
+            ums = timer.run(lambda i: g.replay(), max(5, args.steps // 4), 2)
+            del g
+            uus = ums * 1e3 / n_layers
+            out["batch1"]["unfused"] = dict(launches=nl[0], us_per_block=round(uus, 3),
+                                            over_fused=round(uus / us_block, 3))
     res["moe"] = out
     del pools
     torch.cuda.empty_cache()

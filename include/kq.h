@@ -206,6 +206,25 @@ kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d,
                        void* Y, kq_dtype y_dtype, void* ws, size_t ws_bytes,
                        kq_stream_t stream);
 
+/* The same block with one operation per launch, one token: router logits,
+ * top-k, softmax, then per slot gate GEMV, up GEMV, SwiGLU, and per slot
+ * down GEMV, weighted accumulate -- 3 + 5 * top_k launches (23 at top-4),
+ * every intermediate through `ws`. It exists to measure what the
+ * three-launch block saves. Same arguments and results as kq_moe_block at
+ * batch 1 (other batches: KQ_EUNSUPPORTED); ws needs
+ * kq_moe_unfused_workspace_size bytes, 256-byte aligned, and no
+ * initialisation. n_launches (may be NULL) receives the number of kernel
+ * launches made.
+ * Replaces: encodeUnfused moe-fused/src/main.mm:208-284 and its kernels
+ *   u_router .. u_axpy moe-fused/src/kernels.metal:284-392 (the reference's
+ *   28 launches include five x-sum passes that this GEMV does in-kernel). */
+size_t kq_moe_unfused_workspace_size(const kq_moe_desc* d);
+kq_status kq_moe_block_unfused(const uint8_t* pool, const kq_moe_desc* d,
+                               const void* R, kq_dtype r_dtype, const void* X, kq_dtype x_dtype,
+                               uint32_t batch, uint32_t* idx, float* wgt, uint16_t* xh,
+                               uint16_t* H, void* Y, kq_dtype y_dtype, void* ws, size_t ws_bytes,
+                               uint32_t* n_launches, kq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

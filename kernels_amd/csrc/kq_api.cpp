@@ -304,4 +304,39 @@ kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d, const void* R,
                                            reinterpret_cast<hipStream_t>(stream)));
 }
 
+size_t kq_moe_unfused_workspace_size(const kq_moe_desc* d) {
+    if (check_desc(d, 1) != KQ_OK) return 0;
+    return kq::moe_unfused_ws_bytes(*d);
+}
+
+kq_status kq_moe_block_unfused(const uint8_t* pool, const kq_moe_desc* d, const void* R,
+                               kq_dtype r_dtype, const void* X, kq_dtype x_dtype, uint32_t batch,
+                               uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H, void* Y,
+                               kq_dtype y_dtype, void* ws, size_t ws_bytes, uint32_t* n_launches,
+                               kq_stream_t stream) {
+    kq_status st = check_desc(d, batch);
+    if (st != KQ_OK) return st;
+    if (batch != 1) return KQ_EUNSUPPORTED;
+    if (!pool || !R || !X || !idx || !wgt || !H || !Y) return KQ_ENULL;
+    if (x_dtype == KQ_F32 && !xh) return KQ_ENULL;
+    if (!(r_dtype == KQ_F16 || r_dtype == KQ_F32) || !(x_dtype == KQ_F16 || x_dtype == KQ_F32))
+        return KQ_EUNSUPPORTED;
+    if (!(y_dtype == KQ_F16 || y_dtype == KQ_F32)) return KQ_EUNSUPPORTED;
+    if (!aligned(pool, 16) || !aligned(R, 16) || !aligned(X, 16) || !aligned(idx, 4) ||
+        !aligned(wgt, 4) || !aligned(H, 16))
+        return KQ_EALIGN;
+    if (xh && !aligned(xh, 16)) return KQ_EALIGN;
+    if (!aligned(Y, y_dtype == KQ_F32 ? 4 : 2)) return KQ_EALIGN;
+    if (!ws || ws_bytes < kq::moe_unfused_ws_bytes(*d)) return KQ_EWORKSPACE;
+    if (!aligned(ws, 256)) return KQ_EALIGN;
+    if (!kq::int4_valu_supported(d->hidden, 1, kq::Int4Cfg{0, 0}) ||
+        !kq::int4_valu_supported(d->inter, 1, kq::Int4Cfg{0, 0}))
+        return KQ_EUNSUPPORTED;
+    st = hip_status(kq::launch_moe_unfused(pool, *d, R, r_dtype == KQ_F32, X, x_dtype == KQ_F32,
+                                           idx, wgt, xh, H, Y, y_dtype == KQ_F32, ws,
+                                           reinterpret_cast<hipStream_t>(stream)));
+    if (n_launches) *n_launches = st == KQ_OK ? kq::moe_unfused_launches(*d) : 0;
+    return st;
+}
+
 }  // extern "C"

@@ -48,6 +48,8 @@ struct VArgs {
     uint32_t P, Q, J;                 // K parts, row-group lanes, steps per part
     uint32_t groups_wg, ngroups;      // row groups per workgroup / in total
     uint32_t rounds, nreal, nsteps;   // rounds per workgroup; items per wave, padded to D
+    const uint32_t* gsel;             // gathered form: W, S, B move by gsel[0] * gstride
+    uint64_t gstride;                 // bytes (one matrix of a pool, picked on the device)
 };
 
 struct VPlan {
@@ -95,7 +97,7 @@ __host__ __device__ inline size_t vlds_x(uint32_t ntok, uint32_t nchp) {
 constexpr uint32_t kXBlk = 4608;
 constexpr int kXr = 8;  // x words a thread stages per pass (one pass up to 8 x threads)
 
-template <int NB, int R, int D, bool SB, bool BF>
+template <int NB, int R, int D, bool SB, bool BF, bool GA>
 __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr uint32_t MB = SB ? 4 : 2;  // metadata bytes per group and array
@@ -116,12 +118,18 @@ __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
     const uint32_t row0 = g0 * R;
     const uint32_t rows_wg = min(A.groups_wg * R, A.M - row0);
     const uint32_t rowb = A.K >> 1, metab = A.gpr * MB;
-    const rsrc_t rW = make_rsrc(reinterpret_cast<const unsigned char*>(A.W) + (size_t)row0 * rowb,
-                                rows_wg * rowb);
-    const rsrc_t rS = make_rsrc(reinterpret_cast<const unsigned char*>(A.S) + (size_t)row0 * metab,
-                                rows_wg * metab);
-    const rsrc_t rB = make_rsrc(reinterpret_cast<const unsigned char*>(SB ? A.S : A.B) +
-                                    (size_t)row0 * metab, rows_wg * metab);
+    const unsigned char* bW = reinterpret_cast<const unsigned char*>(A.W);
+    const unsigned char* bS = reinterpret_cast<const unsigned char*>(A.S);
+    const unsigned char* bB = reinterpret_cast<const unsigned char*>(SB ? A.S : A.B);
+    if constexpr (GA) {  // one matrix of a pool, its index written by an earlier launch
+        const size_t go = (size_t)__builtin_amdgcn_readfirstlane(*A.gsel) * A.gstride;
+        bW += go;
+        bS += go;
+        bB += go;
+    }
+    const rsrc_t rW = make_rsrc(bW + (size_t)row0 * rowb, rows_wg * rowb);
+    const rsrc_t rS = make_rsrc(bS + (size_t)row0 * metab, rows_wg * metab);
+    const rsrc_t rB = make_rsrc(bB + (size_t)row0 * metab, rows_wg * metab);
     const rsrc_t rX = make_rsrc(A.X, NB * A.K * 2);
 
     // ---- 1. x staging loads first (vmcnt retires in order), all in one pass
@@ -372,9 +380,9 @@ bool make_vplan(uint32_t M, uint32_t K, uint32_t ntok, Int4Cfg cfg, VPlan& out) 
     return found;
 }
 
-template <int NB, int R, int D, bool SB, bool BF>
+template <int NB, int R, int D, bool SB, bool BF, bool GA>
 hipError_t vgo(const VArgs& a, const VPlan& pl, hipStream_t s) {
-    auto kern = int4_valu<NB, R, D, SB, BF>;
+    auto kern = int4_valu<NB, R, D, SB, BF, GA>;
     if (pl.lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -385,21 +393,21 @@ hipError_t vgo(const VArgs& a, const VPlan& pl, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int NB, int R, bool SB, bool BF>
+template <int NB, int R, bool SB, bool BF, bool GA>
 hipError_t vgo_d(const VArgs& a, const VPlan& pl, hipStream_t s) {
     switch (pl.D) {
-        case 2: return vgo<NB, R, 2, SB, BF>(a, pl, s);
-        case 4: return vgo<NB, R, 4, SB, BF>(a, pl, s);
+        case 2: return vgo<NB, R, 2, SB, BF, GA>(a, pl, s);
+        case 4: return vgo<NB, R, 4, SB, BF, GA>(a, pl, s);
         case 8:
-            if constexpr (R == 1) return vgo<NB, R, 8, SB, BF>(a, pl, s);
+            if constexpr (R == 1) return vgo<NB, R, 8, SB, BF, GA>(a, pl, s);
             else return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }
 
-template <int NB, bool SB, bool BF>
+template <int NB, bool SB, bool BF, bool GA = false>
 hipError_t vgo_r(const VArgs& a, const VPlan& pl, hipStream_t s) {
-    return pl.R == 2 ? vgo_d<NB, 2, SB, BF>(a, pl, s) : vgo_d<NB, 1, SB, BF>(a, pl, s);
+    return pl.R == 2 ? vgo_d<NB, 2, SB, BF, GA>(a, pl, s) : vgo_d<NB, 1, SB, BF, GA>(a, pl, s);
 }
 
 template <int NB>
@@ -425,8 +433,11 @@ bool int4_valu_supported(uint32_t K, uint32_t batch, Int4Cfg cfg) {
 
 hipError_t launch_int4_valu(const uint32_t* W, const uint16_t* S, const uint16_t* B, int meta_kind,
                             bool interleaved, const uint16_t* X, void* Y, bool y_f32, uint32_t M,
-                            uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg, hipStream_t s) {
+                            uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg, hipStream_t s,
+                            const uint32_t* gsel, uint64_t gstride) {
     const size_t ysz = y_f32 ? 4 : 2;
+    // the gathered form is built for the MoE expert layout: one token, split bf16 S and B
+    if (gsel != nullptr && (batch != 1 || interleaved || meta_kind != 1)) return hipErrorInvalidValue;
     for (uint32_t t0 = 0; t0 < batch;) {
         uint32_t nb = batch - t0 >= kMaxNB ? kMaxNB : 1;
         VPlan pl;
@@ -456,9 +467,12 @@ hipError_t launch_int4_valu(const uint32_t* W, const uint16_t* S, const uint16_t
         a.rounds = pl.rounds;
         a.nreal = pl.nreal;
         a.nsteps = pl.nsteps;
+        a.gsel = gsel;
+        a.gstride = gstride;
         const bool bf = meta_kind == 1;
-        const hipError_t e = nb == 2 ? vgo_nb<2>(a, pl, interleaved, bf, s)
-                                     : vgo_nb<1>(a, pl, interleaved, bf, s);
+        const hipError_t e = gsel != nullptr ? vgo_r<1, false, true, true>(a, pl, s)
+                             : nb == 2       ? vgo_nb<2>(a, pl, interleaved, bf, s)
+                                             : vgo_nb<1>(a, pl, interleaved, bf, s);
         if (e != hipSuccess) return e;
         t0 += nb;
     }

@@ -21,9 +21,14 @@ uint32_t cu_count();
 Int4Cfg int4_valu_default(uint32_t M, uint32_t K, uint32_t batch);
 size_t int4_valu_lds_bytes(uint32_t K, uint32_t batch);
 
+// gsel (device pointer, may be null): the kernel reads the matrix index
+// gsel[0] and moves W, S and B by gsel[0] * gstride bytes -- one matrix of a
+// pool chosen by an earlier launch, with no host round trip. Gathered calls
+// take one token and split bf16 S and B (the MoE expert layout).
 hipError_t launch_int4_valu(const uint32_t* W, const uint16_t* S, const uint16_t* B, int meta_kind,
                             bool interleaved, const uint16_t* X, void* Y, bool y_f32, uint32_t M,
-                            uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg, hipStream_t s);
+                            uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg, hipStream_t s,
+                            const uint32_t* gsel = nullptr, uint64_t gstride = 0);
 bool int4_valu_supported(uint32_t K, uint32_t batch, Int4Cfg cfg);
 
 hipError_t launch_int4_mfma(const uint32_t* W, const uint16_t* S, const uint16_t* B, int meta_kind,
@@ -54,6 +59,15 @@ hipError_t launch_moe_down(const uint8_t* pool, const kq_moe_desc& d, const uint
                            const float* wgt, const uint16_t* H, void* Y, bool y_f32,
                            uint32_t batch, hipStream_t s);
 // router logits -> gate/up with in-kernel top-k (publishes idx, wgt) -> down
+// Router logits only (float [batch][n_experts] at ws + 0; xh = half(X) if X is fp32).
+hipError_t launch_moe_logits(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
+                             const kq_moe_desc& d, uint16_t* xh, void* ws, hipStream_t s);
+// One operation per launch, batch 1 (see kq_moe_unfused.hip).
+size_t moe_unfused_ws_bytes(const kq_moe_desc& d);
+uint32_t moe_unfused_launches(const kq_moe_desc& d);
+hipError_t launch_moe_unfused(const uint8_t* pool, const kq_moe_desc& d, const void* R, bool r_f32,
+                              const void* X, bool x_f32, uint32_t* idx, float* wgt, uint16_t* xh,
+                              uint16_t* H, void* Y, bool y_f32, void* ws, hipStream_t s);
 hipError_t launch_moe_block(const uint8_t* pool, const kq_moe_desc& d, const void* R, bool r_f32,
                             const void* X, bool x_f32, uint32_t batch, uint32_t* idx, float* wgt,
                             uint16_t* xh, uint16_t* H, void* Y, bool y_f32, void* ws,

@@ -35,6 +35,7 @@
 // 32-weight chunk.
 #include "kq_device.h"
 #include "kq_internal.h"
+#include "kq_moe_device.h"
 
 namespace kq {
 
@@ -108,41 +109,6 @@ __device__ __forceinline__ void unpack8(const Raw8<F32>& r, float v[8]) {
         v[4] = h2f(r.v.z & 0xFFFF); v[5] = h2f(r.v.z >> 16);
         v[6] = h2f(r.v.w & 0xFFFF); v[7] = h2f(r.v.w >> 16);
     }
-}
-
-// Order key of a candidate: larger key = better. Selectable logits (not NaN,
-// not -inf) map to an order-preserving unsigned code in the high word (always
-// > 0; -0 counts as +0 so equal logits tie), unselectable ones to 0; the low
-// word is ~index, so among equal high words the lowest index is the largest.
-__device__ __forceinline__ uint64_t cand_key(float v, uint32_t e) {
-    uint32_t hi = 0;
-    if (v > -INFINITY) {
-        const uint32_t b = __builtin_bit_cast(uint32_t, v + 0.0f);
-        hi = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    }
-    return ((uint64_t)hi << 32) | (uint32_t)~e;
-}
-
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t k) {
-    const int lo = (int)(uint32_t)k, hi = (int)(uint32_t)(k >> 32);
-    const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROW_MASK, 0xF, false);
-    const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROW_MASK, 0xF, false);
-    const uint64_t o = ((uint64_t)ohi << 32) | olo;
-    return o > k ? o : k;
-}
-
-// Largest key of the wave, uniform (DPP butterfly, then lane 63).
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
-    k = dpp_max_u64<0xB1, 0xF>(k);   // xor 1
-    k = dpp_max_u64<0x4E, 0xF>(k);   // xor 2
-    k = dpp_max_u64<0x124, 0xF>(k);  // row_ror 4
-    k = dpp_max_u64<0x128, 0xF>(k);  // row_ror 8
-    k = dpp_max_u64<0x142, 0xA>(k);  // row_bcast 15
-    k = dpp_max_u64<0x143, 0xC>(k);  // row_bcast 31
-    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)k, 63);
-    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 63);
-    return ((uint64_t)hi << 32) | lo;
 }
 
 // top-k + softmax of one token, one wave (moe-fused/src/kernels.metal:149-162):
@@ -857,13 +823,6 @@ __device__ __forceinline__ float st_dotx(const StDq<J>& q, const StX<J>& x) {
     return acc;
 }
 
-// SwiGLU of the reference (moe-fused/src/kernels.metal:177-215): the gate
-// clamped above at 7, the up value to [-7, 7], alpha 1.702, (up + 1).
-__device__ __forceinline__ float swiglu(float g, float u) {
-    const float gg = fminf(g, 7.0f), uu = fminf(fmaxf(u, -7.0f), 7.0f);
-    return gg * __frcp_rn(1.0f + __expf(-1.702f * gg)) * (uu + 1.0f);
-}
-
 // Gate/up: items are (distinct expert u, row i) in u-major order; workgroup
 // w takes a contiguous range, wave q every kStWaves-th item of it. Half 0
 // reads gate row i, half 1 up row i. XREG (one token): the token's
@@ -1251,6 +1210,11 @@ hipError_t launch_dn(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* 
 }
 
 }  // namespace
+
+hipError_t launch_moe_logits(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
+                             const kq_moe_desc& d, uint16_t* xh, void* ws, hipStream_t s) {
+    return launch_router_t<false>(R, r_f32, X, x_f32, batch, d, xh, ws, nullptr, nullptr, s);
+}
 
 size_t moe_ws_bytes(const kq_moe_desc& d, uint32_t batch) { return ws_layout(d, batch).total; }
 

@@ -131,6 +131,7 @@ struct Variant {
     double bytes = 0;  // per dispatch
     bool check = true;
     double best_s = 0, med_s = 0, relerr = 0;
+    int launches = 1;  // kernel launches per dispatch (reported)
 };
 
 // Dispatches per span chosen so a span lasts ~5 ms (at most 64), as the

@@ -208,11 +208,28 @@ int main(int argc, char** argv) {
         DRV_KQ(kq_moe_down_combine(dpool[layer]->p, &d, dIdx.p, dWgt.p, dH.p, dY.p, KQ_F32, batch, nullptr, 0, ks));
         layer = (layer + 1) % (int)nres;
     };
+    // one operation per launch (encodeUnfused, moe-fused/src/main.mm:208-284); one token only
+    const size_t uwsb = kq_moe_unfused_workspace_size(&d);
+    drv::DevBuf<uint8_t> uws(uwsb ? uwsb : 256);
+    uint32_t nunf = 0;
+    auto unfused = [&](hipStream_t, int) {
+        DRV_KQ(kq_moe_block_unfused(dpool[layer]->p, &d, rptr, rdt, dX.p, KQ_F32, batch, dIdx.p, dWgt.p,
+                                    dXh.p, dH.p, dY.p, KQ_F32, uws.p, uwsb, &nunf, ks));
+        layer = (layer + 1) % (int)nres;
+    };
     std::vector<drv::Variant> vars(2);
     vars[0].name = "fused block (kq_moe_block)";
     vars[0].enc = fused;
+    vars[0].launches = 3;
     vars[1].name = "router, gate_up, down (3 calls)";
     vars[1].enc = three;
+    vars[1].launches = 3;
+    if (batch == 1) {
+        vars.emplace_back();
+        vars[2].name = "unfused (one op per launch)";
+        vars[2].enc = unfused;
+        vars[2].launches = 3 + 5 * (int)TK;
+    }
 
     printf("\ncorrectness vs the fp64 host check (router, top-k, both matmuls, SwiGLU)\n");
     double yinf = 0;
@@ -244,6 +261,10 @@ int main(int argc, char** argv) {
                v.relerr, (idxok && v.relerr < 2e-3) ? "ok" : "FAIL");
         ok = ok && idxok && v.relerr < 2e-3;
     }
+    if (batch == 1 && nunf != (uint32_t)vars[2].launches) {
+        printf("unfused path reported %u launches, expected %d\n", nunf, vars[2].launches);
+        return 1;
+    }
     if (!ok) return 1;
     if (!dump.empty()) {  // results/topk.txt and results/y_metal.f32 of the reference
         FILE* f = fopen((dump + "/topk.txt").c_str(), "w");
@@ -273,12 +294,16 @@ int main(int argc, char** argv) {
     printf("\n%-36s %10s %12s %12s %12s %12s\n", "path", "launches", "us/block", "GB/s", "GB/s(ref)", "tok/s");
     printf("------------------------------------------------------------------------------------------------\n");
     for (const auto& v : vars)
-        printf("  %-34s %10d %12.3f %12.1f %12.1f %12.1f\n", v.name.c_str(), 3, v.best_s * 1e6,
+        printf("  %-34s %10d %12.3f %12.1f %12.1f %12.1f\n", v.name.c_str(), v.launches, v.best_s * 1e6,
                bytes / v.best_s / 1e9, ref_mb / v.best_s / 1e9, batch / (layers * v.best_s));
     printf("------------------------------------------------------------------------------------------------\n");
     const double tb = std::min(vars[0].best_s, vars[1].best_s);
     printf("\nblock time            : %.3f us (median %.3f us)\n", tb * 1e6, vars[0].med_s * 1e6);
     printf("%% of 8 TB/s on bytes read : %.1f%%\n", 100.0 * bytes / tb / 1e9 / drv::kPeakGBs);
+    if (batch == 1)
+        printf("unfused / fused       : %.2fx the time, %d vs %d launches (%.2f us per extra launch)\n",
+               vars[2].best_s / vars[0].best_s, vars[2].launches, vars[0].launches,
+               (vars[2].best_s - vars[0].best_s) * 1e6 / (vars[2].launches - vars[0].launches));
     printf("decode rate           : %.1f tok/s  (%d layers, experts resident, MoE only)\n",
            batch / (layers * tb), layers);
 

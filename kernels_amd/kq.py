@@ -24,7 +24,8 @@ EXPORTS = ("kq_status_str", "kq_last_hip_error", "kq_version", "kq_int4_gemv",
            "kq_int4_gemv_path", "kq_int4_gemv_cfg", "kq_xsum32", "kq_stream_read",
            "kq_vq_gemv", "kq_moe_default_desc", "kq_moe_workspace_size",
            "kq_moe_workspace_init", "kq_moe_router_topk", "kq_moe_gate_up_swiglu",
-           "kq_moe_down_combine", "kq_moe_block")
+           "kq_moe_down_combine", "kq_moe_block", "kq_moe_unfused_workspace_size",
+           "kq_moe_block_unfused")
 
 
 class KQError(RuntimeError):
@@ -82,9 +83,14 @@ def lib():
                                           sz, vp]
         L.kq_moe_block.argtypes = [vp, C.POINTER(MoEDesc), vp, i32, vp, i32, u32, vp, vp, vp, vp,
                                    vp, i32, vp, sz, vp]
+        L.kq_moe_unfused_workspace_size.argtypes = [C.POINTER(MoEDesc)]
+        L.kq_moe_unfused_workspace_size.restype = sz
+        L.kq_moe_block_unfused.argtypes = [vp, C.POINTER(MoEDesc), vp, i32, vp, i32, u32, vp, vp,
+                                           vp, vp, vp, i32, vp, sz, C.POINTER(u32), vp]
         for name in EXPORTS:
             if name not in ("kq_status_str", "kq_last_hip_error", "kq_version",
-                            "kq_moe_default_desc", "kq_moe_workspace_size"):
+                            "kq_moe_default_desc", "kq_moe_workspace_size",
+                            "kq_moe_unfused_workspace_size"):
                 getattr(L, name).restype = i32
         _lib = L
     return _lib
@@ -241,3 +247,22 @@ def moe_block(pool, desc, R, x, idx, wgt, H, y, ws, ws_bytes, batch=1, xh=None, 
     _check(lib().kq_moe_block(_ptr(pool), C.byref(desc), _ptr(R), _dt(R), _ptr(x), _dt(x), batch,
                               _ptr(idx), _ptr(wgt), _ptr(xh), _ptr(H), _ptr(y), _dt(y), _ptr(ws),
                               ws_bytes, _stream(stream)), "kq_moe_block")
+
+
+def moe_unfused_workspace_size(desc):
+    n = lib().kq_moe_unfused_workspace_size(C.byref(desc))
+    if n == 0:
+        raise KQError(KQ_EINVAL, "kq_moe_unfused_workspace_size")
+    return n
+
+
+def moe_block_unfused(pool, desc, R, x, idx, wgt, H, y, ws, ws_bytes, batch=1, xh=None,
+                      stream=None):
+    """encodeUnfused (moe-fused/src/main.mm:208-284): the block one operation
+    per launch. Returns the number of kernel launches it made."""
+    n = C.c_uint32(0)
+    _check(lib().kq_moe_block_unfused(_ptr(pool), C.byref(desc), _ptr(R), _dt(R), _ptr(x), _dt(x),
+                                      batch, _ptr(idx), _ptr(wgt), _ptr(xh), _ptr(H), _ptr(y),
+                                      _dt(y), _ptr(ws), ws_bytes, C.byref(n), _stream(stream)),
+           "kq_moe_block_unfused")
+    return n.value

@@ -123,6 +123,29 @@ def test_moe_rejects_on_host():
     assert L.kq_moe_workspace_init(FAKE + 4, 64, None) == kq.KQ_EALIGN
 
 
+def test_moe_unfused_rejects_on_host():
+    L = kq.lib()
+    d = kq.moe_default_desc()
+    n = kq.moe_unfused_workspace_size(d)
+    assert n >= 4 * (128 + 2 * 2880 + 2 * 2880)
+    cnt = C.c_uint32(7)
+
+    def call(batch=1, ws=FAKE, wsb=n, pool=FAKE, xdt=kq.F16, xh=None):
+        return L.kq_moe_block_unfused(pool, C.byref(d), FAKE, kq.F16, FAKE, xdt, batch, FAKE,
+                                      FAKE, xh, FAKE, FAKE, kq.F32, ws, wsb, C.byref(cnt), None)
+    assert call(batch=2) == kq.KQ_EUNSUPPORTED  # one token, like the reference's unfused path
+    assert call(batch=0) == kq.KQ_EINVAL
+    assert call(wsb=n - 1) == kq.KQ_EWORKSPACE
+    assert call(ws=None) == kq.KQ_EWORKSPACE
+    assert call(ws=FAKE + 16) == kq.KQ_EALIGN
+    assert call(pool=None) == kq.KQ_ENULL
+    assert call(xdt=kq.F32) == kq.KQ_ENULL  # fp32 x needs an xh buffer
+    assert cnt.value == 7  # untouched by a rejected call
+    bad = kq.moe_default_desc()
+    bad.top_k = 9
+    assert L.kq_moe_unfused_workspace_size(C.byref(bad)) == 0
+
+
 def test_stream_read_and_xsum_reject_on_host():
     L = kq.lib()
     assert L.kq_stream_read(FAKE, 100, FAKE, None) == kq.KQ_EINVAL

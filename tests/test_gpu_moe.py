@@ -100,6 +100,11 @@ def test_router_ties_lowest_index(gpu):
     assert np.allclose(b.wgt.cpu().numpy()[0], owgt[0], atol=1e-6)
 
 
+def unfused_ws(device, d):
+    wsb = kq.moe_unfused_workspace_size(d)
+    return torch.empty(wsb, dtype=torch.uint8, device=device), wsb
+
+
 def _pool_desc(n):
     d = kq.moe_default_desc()
     d.n_experts = n
@@ -172,6 +177,20 @@ def test_block_full_pool(gpu, batch):
         assert np.allclose(b.wgt.cpu().numpy(), owgt, atol=1e-6)
         got = to_f64(b.y)
         assert_close(got, Yref, what=f"block batch {batch} rep {rep}")
+        assert inf_rel(got, Yref) < 2e-3
+    if batch == 1:
+        # the same block one operation per launch: same routing, same result
+        u = Block(gpu, d, 1)
+        ws, wsb = unfused_ws(gpu, d)
+        n = kq.moe_block_unfused(pool, d, Rd, Xd, u.idx, u.wgt, u.H, u.y, ws, wsb)
+        torch.cuda.synchronize()
+        assert n == 3 + 5 * d.top_k == 23
+        assert np.array_equal(u.idx.cpu().numpy().astype(np.uint32), oidx)
+        assert np.allclose(u.wgt.cpu().numpy(), owgt, atol=1e-6)
+        Href = oracle.moe_gate_up(host, odesc(d), oidx, X, oracle.F16, 1)
+        assert_close(to_f64(u.H), Href, what="unfused h")
+        got = to_f64(u.y)
+        assert_close(got, Yref, what="unfused block")
         assert inf_rel(got, Yref) < 2e-3
     del pool
 
@@ -288,3 +307,92 @@ def test_other_shapes(gpu, hidden, inter, batch):
     Yd = oracle.moe_down(host, odesc(d), oidx, b.wgt.cpu().numpy().astype(np.float64),
                          host_bits(b.H, np.uint16), batch)
     assert_close(to_f64(b.y), Yd, atol=1e-4, rtol=1e-4, what=f"down {hidden}x{inter} b{batch}")
+
+
+def test_unfused_fp32_inputs_and_fp16_out(gpu, pool16):
+    """The one-op-per-launch block with fp32 router and x (xh written by its
+    router launch) and an fp16 output, against the oracle and the fused
+    block's routing."""
+    host, pool = pool16
+    d = _pool_desc(16)
+    rng = np.random.default_rng(13)
+    R = (rng.normal(0, 0.02, (16, 2880))).astype(np.float32)
+    X = rng.normal(0, 1, (1, 2880)).astype(np.float32)
+    oidx, owgt, lg = oracle.moe_router(R, oracle.F32, X, oracle.F32, 1, odesc(d))
+    assert routing_margin(lg, 4) > 1e-4
+    b = Block(gpu, d, 1, x_f32=True, y_dtype=torch.float16)
+    ws, wsb = unfused_ws(gpu, d)
+    n = kq.moe_block_unfused(pool, d, torch.from_numpy(R).to(gpu), torch.from_numpy(X).to(gpu),
+                             b.idx, b.wgt, b.H, b.y, ws, wsb, xh=b.xh)
+    torch.cuda.synchronize()
+    assert n == 23
+    assert np.array_equal(b.idx.cpu().numpy().astype(np.uint32), oidx)
+    assert np.allclose(b.wgt.cpu().numpy(), owgt, atol=1e-6)
+    assert np.array_equal(host_bits(b.xh, np.uint16), X.astype(np.float16).view(np.uint16))
+    _, _, Yref = oracle.moe_block(host, odesc(d), R, oracle.F32, X, oracle.F32, 1)
+    got = to_f64(b.y)
+    assert inf_rel(got, Yref) < 2e-3
+    assert_close(got, Yref, atol=2e-2, rtol=2e-3, what="fp32-in unfused block")
+
+
+@pytest.mark.parametrize("hidden,inter", [(1024, 2048), (4096, 512), (2048, 4096)])
+def test_unfused_other_shapes(gpu, hidden, inter):
+    """The one-op-per-launch block on other descriptors (16 experts, top-3:
+    3 + 5 * 3 = 18 launches) against the oracle."""
+    d, off = _compact_desc(hidden, inter, 16, 3)
+    host = gen.moe_pool(16, seed=hidden + 2 * inter, quantize=True, hidden=hidden, inter=inter,
+                        blob=d.blob, off=off)
+    pool = dev(host, gpu)
+    R, X = gen.moe_inputs(16, hidden=hidden, batch=1, seed=inter + 7)
+    oidx, owgt, lg = oracle.moe_router(R, oracle.F16, X, oracle.F16, 1, odesc(d))
+    assert routing_margin(lg, 3) > 1e-5
+    _, _, Yref = oracle.moe_block(host, odesc(d), R, oracle.F16, X, oracle.F16, 1)
+    b = Block(gpu, d, 1)
+    ws, wsb = unfused_ws(gpu, d)
+    Rd, Xd = dev(R, gpu).view(torch.float16), dev(X, gpu).view(torch.float16)
+    n = kq.moe_block_unfused(pool, d, Rd, Xd, b.idx, b.wgt, b.H, b.y, ws, wsb)
+    torch.cuda.synchronize()
+    assert n == 18
+    assert np.array_equal(b.idx.cpu().numpy().astype(np.uint32), oidx)
+    assert np.allclose(b.wgt.cpu().numpy(), owgt, atol=1e-6)
+    Href = oracle.moe_gate_up(host, odesc(d), oidx, X, oracle.F16, 1)
+    assert_close(to_f64(b.H), Href, what=f"unfused h {hidden}x{inter}")
+    assert_close(to_f64(b.y), Yref, what=f"unfused block {hidden}x{inter}")
+
+
+def test_unfused_graph_replays(gpu, pool16):
+    """The 23 launches captured in a HIP graph: every replay, with eager calls
+    and synchronisations between replays, equals the eager result bit for
+    bit."""
+    host, pool = pool16
+    d = _pool_desc(16)
+    R, X = gen.moe_inputs(16, batch=1, seed=77)
+    Rd, Xd = dev(R, gpu).view(torch.float16), dev(X, gpu).view(torch.float16)
+    b = Block(gpu, d, 1)
+    ws, wsb = unfused_ws(gpu, d)
+
+    def block():
+        kq.moe_block_unfused(pool, d, Rd, Xd, b.idx, b.wgt, b.H, b.y, ws, wsb)
+
+    block()
+    torch.cuda.synchronize()
+    ref_idx, ref_y = b.idx.clone(), b.y.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        block()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        block()
+    for rep in range(3):
+        b.y.fill_(float("nan"))
+        b.idx.fill_(-1)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(b.idx, ref_idx), f"replay {rep} idx"
+        assert torch.equal(b.y, ref_y), f"replay {rep} y"
+        block()
+        torch.cuda.synchronize()
+        assert torch.equal(b.y, ref_y), f"eager after replay {rep}"
