@@ -401,13 +401,27 @@ def cpu_baseline(seconds):
         if el >= seconds:
             break
     layer_s = el / n
+    # the fp64 oracle (the reference's host check, int4-gemv/src/main.mm:64-92)
+    # on the same cores, over a shorter sample of the same layers
+    n64, t0 = 0, time.perf_counter()
+    while True:
+        W, SB, X, M, K = mats[n64 % ncopy][n64 % len(LLAMA)]
+        oracle.int4_gemv(W, SB, None, X, M, K, G, True, nthreads=cores)
+        n64 += 1
+        el64 = time.perf_counter() - t0
+        if el64 >= seconds / 3 and n64 >= len(LLAMA):
+            break
+    b64 = sum(int4_bytes(*LLAMA[i % len(LLAMA)][1:]) for i in range(n64))
+    fp64 = {"value": round(b64 / el64 / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "sample": f"{n64} GEMVs of the Llama layer shapes in {el64:.1f} s"}
     return {"value": round(step_bytes / layer_s / 1e9, 2), "unit": "GB/s", "cores": cores,
             "kind": "port",
             "sample": f"{n} Llama-3-8B layers (7 int4 GEMVs each, {step_bytes / 1e6:.1f} MB) "
                       f"over {ncopy} weight copies in {el:.1f} s; x86 AVX2+F16C restatement of "
                       f"cpu_gemv_neon (hetero-gemv/src/cpu_gemv.h:88-103)",
             "ms_per_layer": round(layer_s * 1e3, 3),
-            "ms_per_step_32_layers": round(layer_s * 1e3 * N_LAYERS, 2)}
+            "ms_per_step_32_layers": round(layer_s * 1e3 * N_LAYERS, 2),
+            "fp64_oracle": fp64}
 
 
 def main():
