@@ -112,70 +112,50 @@ __device__ __forceinline__ void unpack8(const Raw8<F32>& r, float v[8]) {
 }
 
 // top-k + softmax of one token, one wave (moe-fused/src/kernels.metal:149-162):
-// k passes of "strictly greater wins, ascending scan" -- ties go to the lowest
-// index, NaN and -inf are never selectable, a pass with nothing selectable
-// picks expert 0 -- then softmax over the chosen logits. Up to 256 experts
-// (4 per lane); the passes are DPP reductions of cand_key, no LDS traffic.
-// COHERENT: the logits come from other workgroups of the same launch
-// (device-coherent loads); otherwise from an earlier launch (plain loads).
+// the selection of topk_select over the token's logits (4 per lane), then
+// the softmax of the selected logits. COHERENT: the logits come from other
+// workgroups of the same launch (device-coherent loads); otherwise from an
+// earlier launch (plain loads).
 template <bool COHERENT>
 __device__ void topk_wave(const float* L, uint32_t NE, uint32_t TK,
                           uint32_t* idx_out, float* wgt_out) {
     const uint32_t lane = threadIdx.x & 63;
     float v[4];
-    uint64_t key[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t ei = lane + 64 * q;
+        float x;
         if constexpr (COHERENT)
-            v[q] = __hip_atomic_load(L + min(ei, NE - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            x = __hip_atomic_load(L + min(ei, NE - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else
-            v[q] = L[min(ei, NE - 1)];
-        key[q] = ei < NE ? cand_key(v[q], ei) : 0;  // past NE: never the best (index ~ei > NE)
+            x = L[min(ei, NE - 1)];
+        v[q] = cand(x, ei < NE);
     }
     float chosen[kMaxTopK];
     uint32_t pick[kMaxTopK];
+    topk_select(v, TK, pick, chosen);
+    // softmax over the selected logits, slot j in lane j: one exp per lane and
+    // a three-step sum instead of a serial chain in one lane
+    float mx = chosen[0], cj = -INFINITY;
+    uint32_t pj = 0;
 #pragma unroll
     for (int j = 0; j < kMaxTopK; ++j) {
-        chosen[j] = -INFINITY;
-        pick[j] = 0;
         if ((uint32_t)j < TK) {
-            uint64_t best = key[0];
-#pragma unroll
-            for (int q = 1; q < 4; ++q) best = key[q] > best ? key[q] : best;
-            best = wave_max_key(best);
-            uint32_t bi = ~(uint32_t)best;
-            float bv = -INFINITY;
-            if ((uint32_t)(best >> 32) == 0) {
-                bi = 0;  // nothing selectable
-            } else {
-                const uint32_t qb = (bi >> 6) & 3;  // uniform: select, no dynamic indexing
-                const float src = qb == 0 ? v[0] : qb == 1 ? v[1] : qb == 2 ? v[2] : v[3];
-                bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                   __builtin_bit_cast(int, src), bi & 63));
+            mx = fmaxf(mx, chosen[j]);
+            if (lane == (uint32_t)j) {
+                cj = chosen[j];
+                pj = pick[j];
             }
-            chosen[j] = bv;
-            pick[j] = bi;
-            // the winner's logit becomes -inf (unselectable) for later passes
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                if (lane + 64 * q == bi) key[q] = (uint64_t)(uint32_t)~bi;
         }
     }
-    if (lane == 0) {
-        float mx = chosen[0];
-#pragma unroll
-        for (int j = 1; j < kMaxTopK; ++j)
-            if ((uint32_t)j < TK) mx = fmaxf(mx, chosen[j]);
-        float ex[kMaxTopK], sum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kMaxTopK; ++j) {
-            ex[j] = 0.0f;
-            if ((uint32_t)j < TK) { ex[j] = expf(chosen[j] - mx); sum += ex[j]; }
-        }
-#pragma unroll
-        for (int j = 0; j < kMaxTopK; ++j)
-            if ((uint32_t)j < TK) { idx_out[j] = pick[j]; wgt_out[j] = ex[j] / sum; }
+    const float ex = lane < TK ? __expf(cj - mx) : 0.0f;
+    float sum = ex;
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 4);
+    if (lane < TK) {
+        idx_out[lane] = pj;
+        wgt_out[lane] = __fdividef(ex, sum);
     }
 }
 
@@ -431,59 +411,62 @@ __device__ void get_plan(const Plan* plan_g, const uint32_t* idx, const float* w
     }
 }
 
-// The router's tail run by a workgroup of the next launch: top-k + softmax of
-// every token from the logits lg (one wave per token), then the plan;
-// workgroup 0 publishes idx, wgt and the plan for the down launch.
+// The router's tail run by every wave of the next launch: top-k + softmax of
+// every token from the logits lg, then the plan. Every wave computes the same
+// values and writes the same LDS words, so each wave can use its own results
+// without a workgroup barrier and issue its weight loads at once. The plan
+// lists the distinct experts in the order of their first slot (the down
+// launch reads the same plan, so any fixed order gives the same result):
+// at one token the top-k experts are distinct and slot s is plan entry s.
+// At most kPlanSlots slots (the launcher's limit), lane s takes slot s.
+constexpr uint32_t kPlanSlots = 2 * kMaxTopK;
 __device__ void plan_from_logits(const float* lg, uint32_t batch, uint32_t NE, uint32_t TK,
-                                 Plan& ps, uint32_t* s_idx, float* s_wgt, uint32_t* bits,
-                                 uint32_t* idx_out, float* wgt_out, Plan* plan_out) {
-    const uint32_t tid = threadIdx.x;
-    for (uint32_t t = tid >> 6; t < batch; t += blockDim.x >> 6)
+                                 Plan& ps, uint32_t* s_idx, float* s_wgt) {
+    const uint32_t lane = threadIdx.x & 63;
+    for (uint32_t t = 0; t < batch; ++t)
         topk_wave<false>(lg + (size_t)t * NE, NE, TK, s_idx + t * TK, s_wgt + t * TK);
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();
     const uint32_t nslots = batch * TK;
-    if (nslots <= 64) {
-        // one wave: lane s holds slot s's expert; the distinct experts in
-        // ascending order, each with the mask of its slots (as build_plan)
-        if (tid < 64) {
-            const uint32_t e = tid < nslots ? min(s_idx[tid], NE - 1) : 0xFFFFFFFFu;
-            uint64_t m = 0;
-            uint32_t rank = 0;
-            bool first = true;
-            for (uint32_t s2 = 0; s2 < nslots; ++s2) {
-                const uint32_t e2 = __builtin_amdgcn_readlane(e, s2);
-                uint32_t f2 = 1;  // slot s2 is its expert's first slot
-                for (uint32_t s3 = 0; s3 < s2; ++s3)
-                    f2 &= __builtin_amdgcn_readlane(e, s3) != e2 ? 1u : 0u;
-                if (e2 == e) {
-                    m |= 1ull << s2;
-                    if (s2 < tid) first = false;
-                }
-                if (f2 && e2 < e) ++rank;
+    const uint32_t e = lane < nslots ? min(s_idx[lane], NE - 1) : 0xFFFFFFFFu;
+    bool first = lane < nslots;
+    uint64_t m = first ? 1ull << lane : 0ull;
+    if (batch > 1) {  // later tokens may repeat an expert: one plan entry per expert
+        m = 0;
+        for (uint32_t s2 = 0; s2 < nslots; ++s2) {
+            const uint32_t e2 = __builtin_amdgcn_readlane(e, s2);
+            if (e2 == e) {
+                m |= 1ull << s2;
+                if (s2 < lane) first = false;
             }
-            if (tid < nslots && first) {
-                ps.expert[rank] = e;
-                ps.mask[rank][0] = m;
-                ps.mask[rank][1] = 0;
-            }
-            const uint64_t firsts = __ballot(tid < nslots && first);
-            if (tid == 0) ps.n = __popcll(firsts);
         }
-        __syncthreads();
-    } else {
-        build_plan(s_idx, nslots, NE, ps, bits);
     }
-    if (blockIdx.x == 0) {
-        if (tid < nslots) {
-            idx_out[tid] = s_idx[tid];
-            wgt_out[tid] = s_wgt[tid];
-        }
-        if (tid == 0) plan_out->n = ps.n;
-        for (uint32_t u = tid; u < ps.n; u += blockDim.x) {
-            plan_out->expert[u] = ps.expert[u];
-            plan_out->mask[u][0] = ps.mask[u][0];
-            plan_out->mask[u][1] = ps.mask[u][1];
-        }
+    const uint64_t firsts = __ballot(first);
+    if (first) {
+        const uint32_t rank = __popcll(firsts & ((1ull << lane) - 1ull));
+        ps.expert[rank] = e;
+        ps.mask[rank][0] = m;
+        ps.mask[rank][1] = 0;
+    }
+    if (lane == 0) ps.n = __popcll(firsts);
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Workgroup 0 of the gate/up launch publishes idx, wgt and the plan for the
+// down launch (after its own weight loads are issued).
+__device__ void publish_plan(const Plan& ps, const uint32_t* s_idx, const float* s_wgt,
+                             uint32_t nslots, uint32_t* idx_out, float* wgt_out,
+                             Plan* plan_out) {
+    const uint32_t tid = threadIdx.x;
+    if (tid < nslots) {
+        idx_out[tid] = s_idx[tid];
+        wgt_out[tid] = s_wgt[tid];
+    }
+    const uint32_t n = ps.n;
+    if (tid == 0) plan_out->n = n;
+    for (uint32_t u = tid; u < n; u += blockDim.x) {
+        plan_out->expert[u] = ps.expert[u];
+        plan_out->mask[u][0] = ps.mask[u][0];
+        plan_out->mask[u][1] = ps.mask[u][1];
     }
 }
 
@@ -847,8 +830,7 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     StStage st;
     st_stage_load(st, xh, batch, K);
     if constexpr (SRC == 2)
-        plan_from_logits(lg, batch, d.n_experts, TK, ps, s_idx, s_wgt, bits, idx_out, wgt_out,
-                         plan_out);
+        plan_from_logits(lg, batch, d.n_experts, TK, ps, s_idx, s_wgt);
     else
         get_plan<SRC == 1>(plan_g, idx, nullptr, batch * TK, d.n_experts, ps, s_idx, s_wgt, bits);
     const uint32_t nexp = ps.n, N = nexp * IN;
@@ -888,6 +870,9 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
             issue(ring[s]);
             __builtin_amdgcn_sched_barrier(0);
         }
+    }
+    if constexpr (SRC == 2) {
+        if (blockIdx.x == 0) publish_plan(ps, s_idx, s_wgt, batch * TK, idx_out, wgt_out, plan_out);
     }
     st_stage_store<J>(st, act, batch, K);
     __syncthreads();
@@ -1148,6 +1133,7 @@ hipError_t go_dn_st(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* i
 // Streaming gate/up: measured (gpt-oss shapes) 12.0 us vs per-tile 13.9 us
 // at one token; at 8 tokens the per-tile kernel wins (69.5 vs 78.5 us).
 bool gu_streams(const kq_moe_desc& d, uint32_t batch) {
+    // batch * top_k <= kPlanSlots: the in-kernel top-k's plan limit
     return batch <= 2 && st_ok(d, batch, d.hidden, 0);
 }
 

@@ -1,44 +1,70 @@
 // kq_moe_device.h -- device helpers shared by the three-launch MoE block
 // (kq_moe.hip) and its one-op-per-launch form (kq_moe_unfused.hip): the
-// wave argmax of the router top-k and the SwiGLU activation.
+// wave top-k selection of the router and the SwiGLU activation.
 #pragma once
 #include "kq_device.h"
 
 namespace kq {
 
-// Order key of a candidate: larger key = better. Selectable logits (not NaN,
-// not -inf) map to an order-preserving unsigned code in the high word (always
-// > 0; -0 counts as +0 so equal logits tie), unselectable ones to 0; the low
-// word is ~index, so among equal high words the lowest index is the largest.
-__device__ __forceinline__ uint64_t cand_key(float v, uint32_t e) {
-    uint32_t hi = 0;
-    if (v > -INFINITY) {
-        const uint32_t b = __builtin_bit_cast(uint32_t, v + 0.0f);
-        hi = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    }
-    return ((uint64_t)hi << 32) | (uint32_t)~e;
+// Candidate logit as the selection sees it: NaN, -inf and past-the-end
+// experts are never selectable (-inf); -0 counts as +0, so equal logits tie.
+__device__ __forceinline__ float cand(float v, bool valid) {
+    return valid && v > -INFINITY ? v + 0.0f : -INFINITY;
 }
 
 template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t k) {
-    const int lo = (int)(uint32_t)k, hi = (int)(uint32_t)(k >> 32);
-    const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROW_MASK, 0xF, false);
-    const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROW_MASK, 0xF, false);
-    const uint64_t o = ((uint64_t)ohi << 32) | olo;
-    return o > k ? o : k;
+__device__ __forceinline__ float dpp_fmax(float x) {
+    const int xi = __builtin_bit_cast(int, x);
+    const int o = __builtin_amdgcn_update_dpp(xi, xi, CTRL, ROW_MASK, 0xF, false);
+    return fmaxf(x, __builtin_bit_cast(float, o));
 }
 
-// Largest key of the wave, uniform (DPP butterfly, then lane 63).
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
-    k = dpp_max_u64<0xB1, 0xF>(k);   // xor 1
-    k = dpp_max_u64<0x4E, 0xF>(k);   // xor 2
-    k = dpp_max_u64<0x124, 0xF>(k);  // row_ror 4
-    k = dpp_max_u64<0x128, 0xF>(k);  // row_ror 8
-    k = dpp_max_u64<0x142, 0xA>(k);  // row_bcast 15
-    k = dpp_max_u64<0x143, 0xC>(k);  // row_bcast 31
-    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)k, 63);
-    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 63);
-    return ((uint64_t)hi << 32) | lo;
+// Largest value of the wave, uniform (DPP butterfly, then lane 63).
+__device__ __forceinline__ float wave_max_f32(float x) {
+    x = dpp_fmax<0xB1, 0xF>(x);   // xor 1
+    x = dpp_fmax<0x4E, 0xF>(x);   // xor 2
+    x = dpp_fmax<0x124, 0xF>(x);  // row_ror 4
+    x = dpp_fmax<0x128, 0xF>(x);  // row_ror 8
+    x = dpp_fmax<0x142, 0xA>(x);  // row_bcast 15
+    x = dpp_fmax<0x143, 0xC>(x);  // row_bcast 31
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+
+// Top-k by repeated argmax over one wave's candidates, v[q] = the logit of
+// expert lane + 64 q (as cand() maps it), as the reference does it
+// (moe-fused/src/kernels.metal:149-156): pass j takes the largest remaining
+// value -- the lowest index among equal values, as a strictly-greater
+// ascending scan does -- and removes it; a pass with nothing selectable
+// yields index 0 and -inf. Each pass is one float max reduction and a ballot
+// per candidate column (lowest column first, then lowest lane). pick[] and
+// chosen[] are uniform.
+template <int KMAX>
+__device__ __forceinline__ void topk_select(float (&v)[4], uint32_t TK, uint32_t (&pick)[KMAX],
+                                            float (&chosen)[KMAX]) {
+    const uint32_t lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+        pick[j] = 0;
+        chosen[j] = -INFINITY;
+        if ((uint32_t)j >= TK) continue;  // uniform
+        const float mx = wave_max_f32(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+        if (mx == -INFINITY) continue;  // nothing selectable (uniform)
+        uint32_t bi = 0;
+        bool found = false;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint64_t b = __ballot(v[q] == mx);
+            if (!found && b != 0) {
+                bi = 64 * q + (uint32_t)__builtin_ctzll(b);
+                found = true;
+            }
+        }
+        pick[j] = bi;
+        chosen[j] = mx;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (lane + 64 * q == bi) v[q] = -INFINITY;
+    }
 }
 
 // SwiGLU of the reference (moe-fused/src/kernels.metal:177-215): the gate

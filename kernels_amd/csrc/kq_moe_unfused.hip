@@ -51,40 +51,26 @@ UWs uws_layout(const kq_moe_desc& d) {
 // j picks the largest remaining logit, strictly greater wins so ties go to
 // the lowest index, and the winner is removed. NaN and -inf are never
 // selectable; a pass with nothing selectable yields index 0 and -inf, as the
-// block's router does. One wave, up to 4 logits per lane.
+// block's router does (the same topk_select). One wave, up to 4 logits per
+// lane; slot j is written by lane j.
 __global__ __launch_bounds__(64) void u_topk_k(const float* __restrict__ lg, uint32_t NE,
                                                uint32_t TK, uint32_t* __restrict__ idx,
                                                float* __restrict__ sel) {
     const uint32_t lane = threadIdx.x;
     float v[4];
-    uint64_t key[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t ei = lane + 64 * q;
-        v[q] = lg[min(ei, NE - 1)];
-        key[q] = ei < NE ? cand_key(v[q], ei) : 0;
+        v[q] = cand(lg[min(ei, NE - 1)], ei < NE);
     }
-    for (uint32_t j = 0; j < TK; ++j) {
-        uint64_t best = key[0];
+    float chosen[kUMaxTopK];
+    uint32_t pick[kUMaxTopK];
+    topk_select(v, TK, pick, chosen);
 #pragma unroll
-        for (int q = 1; q < 4; ++q) best = key[q] > best ? key[q] : best;
-        best = wave_max_key(best);
-        uint32_t bi = ~(uint32_t)best;
-        float bv = -INFINITY;
-        if ((uint32_t)(best >> 32) == 0) {
-            bi = 0;
-        } else {
-            const uint32_t qb = (bi >> 6) & 3;
-            const float src = qb == 0 ? v[0] : qb == 1 ? v[1] : qb == 2 ? v[2] : v[3];
-            bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, src),
-                                                                     bi & 63));
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (lane + 64 * q == bi) key[q] = (uint64_t)(uint32_t)~bi;
-        if (lane == 0) {
-            idx[j] = bi;
-            sel[j] = bv;
+    for (uint32_t j = 0; j < kUMaxTopK; ++j) {
+        if (j < TK && lane == j) {
+            idx[j] = pick[j];
+            sel[j] = chosen[j];
         }
     }
 }
