@@ -338,6 +338,23 @@ def bench_vq(torch, kq, dev, args, timer, res):
         out[f"{M}x{K}"] = dict(us=round(us, 3), gbs=round(b / us / 1e3, 1),
                                frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4), bytes=b)
         del mats, g
+    # the quantiser that makes this format (vq-gemv/quant/pq_quantize.py:28-83)
+    # from dense N(0, 0.02) weights: 14336 x 4096, reference defaults (25
+    # iterations, 200000-point sample), both formats
+    M, K = 14336, 4096
+    W = torch.randn((M, K), device=dev, generator=gen) * 0.02
+    for name, R, G in (("cb256_rowscale", 256, K), ("reference_cb1_g32", M, 32)):
+        nblk = (M + R - 1) // R
+        IDX = torch.empty((M, K // 2), dtype=torch.uint8, device=dev)
+        C = torch.empty((nblk, 256, 2), dtype=torch.float16, device=dev)
+        S = torch.empty((M, K // G), dtype=torch.float16, device=dev)
+        wsb = kq.vq_quantize_workspace_size(M, K, R, G)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        kq.vq_quantize(W, IDX, C, S, M, K, R, G, ws, wsb)
+        ms = timer.run(lambda i: kq.vq_quantize(W, IDX, C, S, M, K, R, G, ws, wsb), 3, 1)
+        out[f"quantize_{M}x{K}_{name}"] = dict(ms=round(ms, 3), iters=25, sample=200_000,
+                                               launches=3 + 2 * 25)
+    del W
     res["vq"] = out
 
 

@@ -133,6 +133,39 @@ kq_status kq_vq_gemv(const uint8_t* IDX, const uint16_t* C, const uint16_t* S,
                      uint32_t batch, kq_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * VQ quantiser: a dense weight matrix into the format kq_vq_gemv reads
+ *
+ * W: [M][K] of w_dtype (KQ_F32, KQ_F16 or KQ_BF16; finite values).
+ * Out: IDX u8 [M][K/2], C fp16 [ceil(M/rows_per_cb)][256][2] (one codebook
+ * per block of rows_per_cb rows; rows_per_cb >= M is the reference's one
+ * codebook per matrix), S fp16 [M][K/scale_group] (per-group abs-max;
+ * scale_group = 32 is the reference format, = K one scale per row).
+ * Per block: Lloyd's k-means with 256 codewords on the pairs normalised by
+ * their group's scale -- all of the block's pairs, or `sample` of them drawn
+ * with replacement when there are more -- 256 initial centroids drawn from
+ * that sample, `iters` iterations, then every pair to its nearest centroid.
+ * The draws are seeded (splitmix64 of seed, block and draw number) and the
+ * cluster sums are exact integer sums, so the output is a function of the
+ * arguments (the same on every run and device).
+ * Constraints: K % 32 == 0; scale_group == K or a power of two >= 32
+ * dividing K; 1 <= sample <= 2^24; iters <= 1000; min(rows_per_cb, M) * K / 2
+ * < 2^32 and ceil(M / rows_per_cb) <= 65535 (else KQ_EUNSUPPORTED).
+ * ws: kq_vq_quantize_workspace_size bytes, 256-byte aligned (the scales,
+ * the sample, the centroids and their sums); 0 means invalid arguments.
+ * Launches: 3 + 2 * iters.
+ *
+ * Replaces: quantize_matrix / _kmeans vq-gemv/quant/pq_quantize.py:28-83
+ *   (reference defaults: iters 25, sample 200000, scale_group 32,
+ *   rows_per_cb = M).
+ * ------------------------------------------------------------------------ */
+size_t kq_vq_quantize_workspace_size(uint32_t M, uint32_t K, uint32_t rows_per_cb,
+                                     uint32_t scale_group, uint32_t sample);
+kq_status kq_vq_quantize(const void* W, kq_dtype w_dtype, uint32_t M, uint32_t K,
+                         uint32_t rows_per_cb, uint32_t scale_group, uint32_t iters,
+                         uint32_t sample, uint64_t seed, uint8_t* IDX, uint16_t* C, uint16_t* S,
+                         void* ws, size_t ws_bytes, kq_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * MoE decode block (gpt-oss expert-blob format)
  *
  * pool: n_experts blobs of `blob` bytes. Within a blob, projection p (gate,

@@ -309,6 +309,46 @@ size_t kq_moe_unfused_workspace_size(const kq_moe_desc* d) {
     return kq::moe_unfused_ws_bytes(*d);
 }
 
+namespace {
+kq_status check_vq_quant(uint32_t M, uint32_t K, uint32_t rows_per_cb, uint32_t scale_group,
+                         uint32_t sample) {
+    if (M == 0 || K == 0 || K % 32 || rows_per_cb == 0) return KQ_EINVAL;
+    if (!(scale_group == K || (scale_group >= 32 && (scale_group & (scale_group - 1)) == 0 &&
+                               K % scale_group == 0)))
+        return KQ_EINVAL;
+    if (sample == 0 || sample > (1u << 24)) return KQ_EINVAL;
+    const uint64_t rows = rows_per_cb < M ? rows_per_cb : M;
+    if (rows * (K / 2) >= (1ull << 32)) return KQ_EUNSUPPORTED;  // pair indices are 32-bit
+    if ((M + (uint64_t)rows_per_cb - 1) / rows_per_cb > 65535) return KQ_EUNSUPPORTED;
+    return KQ_OK;
+}
+}  // namespace
+
+size_t kq_vq_quantize_workspace_size(uint32_t M, uint32_t K, uint32_t rows_per_cb,
+                                     uint32_t scale_group, uint32_t sample) {
+    if (check_vq_quant(M, K, rows_per_cb, scale_group, sample) != KQ_OK) return 0;
+    return kq::vq_quant_ws_bytes(M, K, scale_group, rows_per_cb, sample);
+}
+
+kq_status kq_vq_quantize(const void* W, kq_dtype w_dtype, uint32_t M, uint32_t K,
+                         uint32_t rows_per_cb, uint32_t scale_group, uint32_t iters,
+                         uint32_t sample, uint64_t seed, uint8_t* IDX, uint16_t* C, uint16_t* S,
+                         void* ws, size_t ws_bytes, kq_stream_t stream) {
+    kq_status st = check_vq_quant(M, K, rows_per_cb, scale_group, sample);
+    if (st != KQ_OK) return st;
+    if (iters > 1000) return KQ_EINVAL;
+    if (!(w_dtype == KQ_F32 || w_dtype == KQ_F16 || w_dtype == KQ_BF16)) return KQ_EUNSUPPORTED;
+    if (!W || !IDX || !C || !S) return KQ_ENULL;
+    if (!ws || ws_bytes < kq::vq_quant_ws_bytes(M, K, scale_group, rows_per_cb, sample))
+        return KQ_EWORKSPACE;
+    if (!aligned(W, w_dtype == KQ_F32 ? 4 : 2) || !aligned(IDX, 4) || !aligned(C, 2) ||
+        !aligned(S, 2) || !aligned(ws, 256))
+        return KQ_EALIGN;
+    return hip_status(kq::launch_vq_quantize(W, (int)w_dtype, M, K, rows_per_cb, scale_group,
+                                             iters, sample, seed, IDX, C, S, ws,
+                                             reinterpret_cast<hipStream_t>(stream)));
+}
+
 kq_status kq_moe_block_unfused(const uint8_t* pool, const kq_moe_desc* d, const void* R,
                                kq_dtype r_dtype, const void* X, kq_dtype x_dtype, uint32_t batch,
                                uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H, void* Y,

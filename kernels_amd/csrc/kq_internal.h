@@ -47,6 +47,15 @@ hipError_t launch_vq(const uint8_t* IDX, const uint16_t* C, const uint16_t* S, c
                      void* Y, bool y_f32, uint32_t M, uint32_t K, uint32_t rows_per_cb,
                      uint32_t scale_group, uint32_t batch, hipStream_t s);
 
+// VQ quantiser (kq_vq_quant.hip)
+size_t vq_quant_ws_bytes(uint32_t M, uint32_t K, uint32_t scale_group, uint32_t rows_per_cb,
+                         uint32_t sample);
+uint32_t vq_quant_launches(uint32_t iters);
+hipError_t launch_vq_quantize(const void* W, int w_dtype, uint32_t M, uint32_t K,
+                              uint32_t rows_per_cb, uint32_t scale_group, uint32_t iters,
+                              uint32_t sample, uint64_t seed, uint8_t* IDX, uint16_t* Cb,
+                              uint16_t* S, void* ws, hipStream_t s);
+
 // MoE
 size_t moe_ws_bytes(const kq_moe_desc& d, uint32_t batch);
 hipError_t launch_ws_zero(void* ws, size_t bytes, hipStream_t s);

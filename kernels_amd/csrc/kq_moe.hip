@@ -13,6 +13,10 @@
 //    agent-scope atomics: they bypass the non-coherent per-XCD L2), so no
 //    L2 write-back fence is needed -- measured ~2 us cheaper per block than a
 //    release fence, and cheaper than a separate selection launch.
+//    At 1-2 tokens the block's router stops after the logits instead: every
+//    wave of the streaming gate/up launch runs the top-k and builds the plan
+//    itself (no barrier before its weight loads), and workgroup 0 publishes
+//    idx, wgt and the plan for down.
 // 2. gate/up + SwiGLU, and 3. down + weighted combine, each in one of two
 //    forms:
 //    - streaming (moe_gu_stream_k up to 2 tokens, moe_dn_stream_k while the

@@ -25,7 +25,7 @@ EXPORTS = ("kq_status_str", "kq_last_hip_error", "kq_version", "kq_int4_gemv",
            "kq_vq_gemv", "kq_moe_default_desc", "kq_moe_workspace_size",
            "kq_moe_workspace_init", "kq_moe_router_topk", "kq_moe_gate_up_swiglu",
            "kq_moe_down_combine", "kq_moe_block", "kq_moe_unfused_workspace_size",
-           "kq_moe_block_unfused")
+           "kq_moe_block_unfused", "kq_vq_quantize_workspace_size", "kq_vq_quantize")
 
 
 class KQError(RuntimeError):
@@ -87,10 +87,14 @@ def lib():
         L.kq_moe_unfused_workspace_size.restype = sz
         L.kq_moe_block_unfused.argtypes = [vp, C.POINTER(MoEDesc), vp, i32, vp, i32, u32, vp, vp,
                                            vp, vp, vp, i32, vp, sz, C.POINTER(u32), vp]
+        L.kq_vq_quantize_workspace_size.argtypes = [u32, u32, u32, u32, u32]
+        L.kq_vq_quantize_workspace_size.restype = sz
+        L.kq_vq_quantize.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, C.c_uint64, vp, vp,
+                                     vp, vp, sz, vp]
         for name in EXPORTS:
             if name not in ("kq_status_str", "kq_last_hip_error", "kq_version",
                             "kq_moe_default_desc", "kq_moe_workspace_size",
-                            "kq_moe_unfused_workspace_size"):
+                            "kq_moe_unfused_workspace_size", "kq_vq_quantize_workspace_size"):
                 getattr(L, name).restype = i32
         _lib = L
     return _lib
@@ -201,6 +205,24 @@ class VQParams:
 def vq_gemv(IDX, Cb, S, x, y, P: VQParams, batch=1, stream=None):
     _check(lib().kq_vq_gemv(_ptr(IDX), _ptr(Cb), _ptr(S), _ptr(x), _ptr(y), _dt(y), P.M, P.K,
                             P.rows_per_cb, P.scale_group, batch, _stream(stream)), "kq_vq_gemv")
+
+
+def vq_quantize_workspace_size(M, K, rows_per_cb, scale_group, sample=200_000):
+    n = lib().kq_vq_quantize_workspace_size(M, K, rows_per_cb, scale_group, sample)
+    if n == 0:
+        raise KQError(KQ_EINVAL, "kq_vq_quantize_workspace_size")
+    return n
+
+
+def vq_quantize(W, IDX, Cb, S, M, K, rows_per_cb, scale_group, ws, ws_bytes, iters=25,
+                sample=200_000, seed=0, w_dtype=None, stream=None):
+    """quantize_matrix (vq-gemv/quant/pq_quantize.py:28-83) on the GPU: W
+    [M][K] (float32, float16 or bfloat16 tensor) into IDX u8 [M][K/2], Cb
+    fp16 [blocks][256][2] and S fp16 [M][K/scale_group]."""
+    _check(lib().kq_vq_quantize(_ptr(W), _dt(W) if w_dtype is None else w_dtype, M, K,
+                                rows_per_cb, scale_group, iters, sample, seed, _ptr(IDX),
+                                _ptr(Cb), _ptr(S), _ptr(ws), ws_bytes, _stream(stream)),
+           "kq_vq_quantize")
 
 
 # ---------------------------------------------------------------------------

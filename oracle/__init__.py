@@ -55,6 +55,16 @@ def lib():
                                           vp, i32]
         L.kqref_int4_gemv_cpu_fast.argtypes = [vp, vp, vp, vp, u32, u32, u32, i32]
         L.kqref_cpu_fast_supported.restype = i32
+        L.kqref_vq_quantize.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, C.c_uint64, vp,
+                                        vp, vp, vp]
+        L.kqref_vq_hash.argtypes = [C.c_uint64, u32, u32]
+        L.kqref_vq_hash.restype = C.c_uint64
+        L.kqref_vq_score.argtypes = [C.c_float] * 4
+        L.kqref_vq_score.restype = C.c_float
+        L.kqref_vq_fix.argtypes = [C.c_float]
+        L.kqref_vq_fix.restype = C.c_int64
+        L.kqref_vq_mean.argtypes = [C.c_int64, C.c_uint64]
+        L.kqref_vq_mean.restype = C.c_float
         _lib = L
     return _lib
 
@@ -176,3 +186,19 @@ def int4_gemv_cpu_fast(W, SB, X, M, K, G, nthreads=0):
     Y = np.zeros(M, np.float32)
     lib().kqref_int4_gemv_cpu_fast(_p(W), _p(SB), _p(X), _p(Y), M, K, G, nthreads)
     return Y
+
+
+def vq_quantize(W, w_dtype, M, K, rows_per_cb, scale_group, iters=25, sample=200_000, seed=0):
+    """VQ quantiser (vq-gemv/quant/pq_quantize.py:28-83 as specified for the
+    GPU). W: float32 [M][K] (w_dtype F32) or uint16 bits (F16 / BF16).
+    Returns (IDX u8 [M][K/2], C fp16 bits [nblk][256][2], S fp16 bits
+    [M][K/scale_group], fp32 centroids [nblk][256][2])."""
+    W = np.ascontiguousarray(W)
+    nblk = (M + rows_per_cb - 1) // rows_per_cb
+    IDX = np.zeros((M, K // 2), np.uint8)
+    Cb = np.zeros((nblk, 256, 2), np.uint16)
+    S = np.zeros((M, K // scale_group), np.uint16)
+    cent = np.zeros((nblk, 256, 2), np.float32)
+    lib().kqref_vq_quantize(_p(W), w_dtype, M, K, rows_per_cb, scale_group, iters, sample, seed,
+                            _p(IDX), _p(Cb), _p(S), _p(cent))
+    return IDX, Cb, S, cent

@@ -1,6 +1,7 @@
 """Build recipe for the CPU oracle (test infrastructure only).
 
-Compiles oracle/kqref.c (fp64 restatement of the reference CPU paths) and
+Compiles oracle/kqref.c (fp64 restatement of the reference CPU paths),
+oracle/vqquant.c (the VQ quantiser as specified for the GPU) and
 oracle/cpu_fast.c (x86 restatement of the reference's CPU int4 GEMV, the timed
 baseline) into oracle/_build/libkqref.so with gcc. No -ffast-math: the oracle
 relies on IEEE fp64 semantics.
@@ -20,7 +21,8 @@ LIB = os.path.join(OUT_DIR, "libkqref.so")
 
 def build(verbose: bool = False) -> str:
     os.makedirs(OUT_DIR, exist_ok=True)
-    srcs = [os.path.join(HERE, "kqref.c"), os.path.join(HERE, "cpu_fast.c")]
+    srcs = [os.path.join(HERE, "kqref.c"), os.path.join(HERE, "vqquant.c"),
+            os.path.join(HERE, "cpu_fast.c")]
     tmp = LIB + ".tmp"
     cmd = ["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-pthread", "-Wall", "-Wextra",
            "-Wno-unused-parameter", "-o", tmp] + srcs + ["-lm"]

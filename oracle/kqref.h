@@ -104,6 +104,19 @@ void kqref_int4_gemv_cpu_fast(const uint32_t* W, const uint16_t* SB, const uint1
 /* 1 if this CPU has AVX2, FMA and F16C (the fast path's requirement). */
 int kqref_cpu_fast_supported(void);
 
+/* VQ quantiser (vqquant.c): quantize_matrix / _kmeans of
+ * vq-gemv/quant/pq_quantize.py:28-83 as specified for the GPU quantiser
+ * (kq_vq_quantize). W: [M][K] of w_dtype; IDX u8 [M][K/2]; Cb fp16
+ * [ceil(M/rows_per_cb)][256][2]; S fp16 [M][K/scale_group]; centroids_out
+ * (may be NULL) receives the fp32 centroids the assignment used. */
+void kqref_vq_quantize(const void* W, int w_dtype, uint32_t M, uint32_t K, uint32_t rows_per_cb,
+                       uint32_t scale_group, uint32_t iters, uint32_t sample, uint64_t seed,
+                       uint8_t* IDX, uint16_t* Cb, uint16_t* S, float* centroids_out);
+uint64_t kqref_vq_hash(uint64_t seed, uint32_t blk, uint32_t j);
+float kqref_vq_score(float px, float py, float cx, float cy);
+int64_t kqref_vq_fix(float v);
+float kqref_vq_mean(int64_t sum, uint64_t cnt);
+
 #ifdef __cplusplus
 }
 #endif

@@ -146,6 +146,31 @@ def test_moe_unfused_rejects_on_host():
     assert L.kq_moe_unfused_workspace_size(C.byref(bad)) == 0
 
 
+def test_vq_quantize_rejects_on_host():
+    L = kq.lib()
+    n = kq.vq_quantize_workspace_size(14336, 4096, 256, 4096, 200_000)
+    # scales + 56 blocks x 200000 sample points + centroids and their sums
+    assert n >= 14336 * 4 + 56 * 200_000 * 8 + 56 * 256 * (8 + 24)
+    assert L.kq_vq_quantize_workspace_size(64, 100, 64, 32, 1000) == 0    # K % 32
+    assert L.kq_vq_quantize_workspace_size(64, 128, 64, 48, 1000) == 0    # group not 2^k
+    assert L.kq_vq_quantize_workspace_size(64, 128, 64, 16, 1000) == 0    # group < 32
+    assert L.kq_vq_quantize_workspace_size(64, 128, 0, 32, 1000) == 0     # rows_per_cb
+    assert L.kq_vq_quantize_workspace_size(64, 128, 64, 32, 0) == 0       # sample
+    assert L.kq_vq_quantize_workspace_size(70000, 128, 1, 32, 10) == 0    # > 65535 blocks
+    m = kq.vq_quantize_workspace_size(64, 128, 64, 32, 1000)
+
+    def call(ws=FAKE, wsb=m, W=FAKE, dt=kq.F32, iters=25, IDX=FAKE):
+        return L.kq_vq_quantize(W, dt, 64, 128, 64, 32, iters, 1000, 0, IDX, FAKE, FAKE, ws, wsb,
+                                None)
+    assert call(wsb=m - 1) == kq.KQ_EWORKSPACE
+    assert call(ws=None) == kq.KQ_EWORKSPACE
+    assert call(W=None) == kq.KQ_ENULL
+    assert call(dt=7) == kq.KQ_EUNSUPPORTED
+    assert call(iters=1001) == kq.KQ_EINVAL
+    assert call(IDX=FAKE + 2) == kq.KQ_EALIGN
+    assert call(ws=FAKE + 64) == kq.KQ_EALIGN
+
+
 def test_stream_read_and_xsum_reject_on_host():
     L = kq.lib()
     assert L.kq_stream_read(FAKE, 100, FAKE, None) == kq.KQ_EINVAL
