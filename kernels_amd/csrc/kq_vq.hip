@@ -52,7 +52,14 @@ struct QArgs {
 struct QPlan {
     uint32_t R, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, ncb;
     size_t lds;
+    uint32_t cr;  // codebook copies in LDS (kCbCopies when they fit, else 1)
 };
+
+// A lookup reads a random codebook entry per lane: with one copy, 64 random
+// indices meet in the 32 LDS banks (measured ~4 extra cycles per lookup).
+// kCbCopies interleaved copies (dword e * 32 + lane % 32) put every lane of a
+// half-wave in its own bank, at 32 KiB per codebook block.
+constexpr uint32_t kCbCopies = 32;
 
 template <int R>
 struct QSlot {
@@ -74,15 +81,14 @@ __host__ __device__ inline size_t qlds_x(uint32_t ntok, uint32_t nchp) {
     return (size_t)ntok * nchp * 64;
 }
 
-// One index word (4 codeword lookups) dotted with its 4 x pairs.
-// (Replicating the 1 KiB codebook per lane to avoid random-index LDS bank
-// conflicts measured no faster: the kernel is bound by instruction issue --
-// extract, address, ds_read and dot2 per codeword -- not by bank conflicts.)
+// One index word (4 codeword lookups) dotted with its 4 x pairs; cbr is the
+// lane's copy of the codebook (CR copies interleaved by dword).
+template <int CR>
 __device__ __forceinline__ float vq_word(uint32_t word, u32x4 xv, const uint32_t* cbr, float acc) {
-    acc = dot2(cbr[word & 0xFF], xv.x, acc);
-    acc = dot2(cbr[(word >> 8) & 0xFF], xv.y, acc);
-    acc = dot2(cbr[(word >> 16) & 0xFF], xv.z, acc);
-    return dot2(cbr[word >> 24], xv.w, acc);
+    acc = dot2(cbr[(word & 0xFF) * CR], xv.x, acc);
+    acc = dot2(cbr[((word >> 8) & 0xFF) * CR], xv.y, acc);
+    acc = dot2(cbr[((word >> 16) & 0xFF) * CR], xv.z, acc);
+    return dot2(cbr[(word >> 24) * CR], xv.w, acc);
 }
 
 // x in LDS: per (step s, token t) one 4096-byte block of four planes (plane
@@ -92,13 +98,13 @@ __device__ __forceinline__ float vq_word(uint32_t word, u32x4 xv, const uint32_t
 constexpr uint32_t kQBlk = 4096;
 constexpr int kQXr = 8;  // x words a thread stages per pass (one pass up to 8 x threads)
 
-template <int NB, int R, int D>
+template <int NB, int R, int D, int CR>
 __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr uint32_t kOOB = 0x80000000u;  // past every descriptor's range: loads read zeros
     const uint32_t nch = A.nch, nchp = A.nchp, nw = A.K >> 3, nstep = nchp >> 6;
-    uint32_t* cb = reinterpret_cast<uint32_t*>(smem + qlds_x(NB, nchp));          // [ncb][256]
-    float* part = reinterpret_cast<float*>(cb + (size_t)A.cb_first_div * 256);  // [rounds][waves][R*NB]
+    uint32_t* cb = reinterpret_cast<uint32_t*>(smem + qlds_x(NB, nchp));  // [ncb][256][CR]
+    float* part = reinterpret_cast<float*>(cb + (size_t)A.cb_first_div * 256 * CR);  // [rounds][waves][R*NB]
 
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
     const uint32_t lane = tid & 63;
@@ -126,15 +132,19 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
             sv[r] = __builtin_amdgcn_raw_buffer_load_b128(rX, w < xtotal ? w * 16 : kOOB, 0, 0);
         }
     }
-    // codebook blocks of this workgroup's rows (at most 4 KiB)
+    // codebook blocks of this workgroup's rows; with CR copies, item i is
+    // entry i / (CR / 4) and stores 4 of its copies
     const uint32_t ncb_total = (A.M + A.rpc - 1) / A.rpc;
     const uint32_t ncb = min(A.cb_first_div, ncb_total - cb0), cbn = ncb * 256;
     const uint32_t* Cw = reinterpret_cast<const uint32_t*>(A.C) + (size_t)cb0 * 256;
-    uint32_t cbv[4];
+    constexpr uint32_t kQd = CR == 1 ? 1 : CR / 4;  // items per entry
+    constexpr int kCbPre = CR == 1 ? 4 : 8;          // items a thread preloads
+    const uint32_t cb_items = cbn * kQd;
+    uint32_t cbv[kCbPre];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < kCbPre; ++r) {
         const uint32_t i = r * nthr + tid;
-        cbv[r] = Cw[i < cbn ? i : cbn - 1];
+        cbv[r] = Cw[i < cb_items ? i / kQd : cbn - 1];
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -201,12 +211,18 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
         *reinterpret_cast<u32x4*>(smem + ((ch >> 6) * NB + t) * kQBlk + jw * 1024 + (ch & 63) * 16) =
             u32x4{0, 0, 0, 0};
     }
+    auto cb_store = [&](uint32_t i, uint32_t v) __attribute__((always_inline)) {
+        if constexpr (CR == 1)
+            cb[i] = v;
+        else
+            *reinterpret_cast<u32x4*>(cb + (i / kQd) * CR + (i % kQd) * 4) = u32x4{v, v, v, v};
+    };
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < kCbPre; ++r) {
         const uint32_t i = r * nthr + tid;
-        if (i < cbn) cb[i] = cbv[r];
+        if (i < cb_items) cb_store(i, cbv[r]);
     }
-    for (uint32_t i = 4 * nthr + tid; i < cbn; i += nthr) cb[i] = Cw[i];  // only if 4 * threads < entries
+    for (uint32_t i = kCbPre * nthr + tid; i < cb_items; i += nthr) cb_store(i, Cw[i / kQd]);
     __syncthreads();
 
     float acc[R][NB];
@@ -266,13 +282,13 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
             uint32_t sr = e.sc[r];
             asm volatile("" : "+v"(iv), "+v"(sr));  // use the loaded values here, not earlier
             const float sc = h2f((uint16_t)sr);
-            const uint32_t* cbr = cb + blk * 256;
+            const uint32_t* cbr = cb + blk * 256 * CR + (CR == 1 ? 0u : (lane & (CR - 1)));
 #pragma unroll
             for (int t = 0; t < NB; ++t) {
-                float da = vq_word(iv.x, xv[t][0], cbr, 0.0f);
-                float db = vq_word(iv.y, xv[t][1], cbr, 0.0f);
-                da = vq_word(iv.z, xv[t][2], cbr, da);
-                db = vq_word(iv.w, xv[t][3], cbr, db);
+                float da = vq_word<CR>(iv.x, xv[t][0], cbr, 0.0f);
+                float db = vq_word<CR>(iv.y, xv[t][1], cbr, 0.0f);
+                da = vq_word<CR>(iv.z, xv[t][2], cbr, da);
+                db = vq_word<CR>(iv.w, xv[t][3], cbr, db);
                 acc[r][t] = fmaf(sc, da + db, acc[r][t]);
             }
         }
@@ -346,16 +362,23 @@ bool make_qplan(uint32_t M, uint32_t K, uint32_t ntok, uint32_t rpc, QPlan& out)
             if (!found || cost < best) {
                 found = true;
                 best = cost;
-                out = QPlan{R, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, ncb, lds};
+                out = QPlan{R, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, ncb, lds, 1};
             }
+        }
+    }
+    if (found) {
+        const size_t rep = out.lds + (size_t)out.ncb * 1024 * (kCbCopies - 1);
+        if (rep <= kLdsMax) {
+            out.lds = rep;
+            out.cr = kCbCopies;
         }
     }
     return found;
 }
 
-template <int NB, int R>
+template <int NB, int R, int CR>
 hipError_t qgo(const QArgs& a, const QPlan& pl, hipStream_t s) {
-    auto kern = vq_valu<NB, R, 2>;
+    auto kern = vq_valu<NB, R, 2, CR>;
     if (pl.lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -368,7 +391,9 @@ hipError_t qgo(const QArgs& a, const QPlan& pl, hipStream_t s) {
 
 template <int NB>
 hipError_t qgo_nb(const QArgs& a, const QPlan& pl, hipStream_t s) {
-    return pl.R == 2 ? qgo<NB, 2>(a, pl, s) : qgo<NB, 1>(a, pl, s);
+    if (pl.cr == kCbCopies)
+        return pl.R == 2 ? qgo<NB, 2, kCbCopies>(a, pl, s) : qgo<NB, 1, kCbCopies>(a, pl, s);
+    return pl.R == 2 ? qgo<NB, 2, 1>(a, pl, s) : qgo<NB, 1, 1>(a, pl, s);
 }
 
 }  // namespace
