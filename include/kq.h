@@ -148,8 +148,9 @@ kq_status kq_vq_gemv(const uint8_t* IDX, const uint16_t* C, const uint16_t* S,
  * cluster sums are exact integer sums, so the output is a function of the
  * arguments (the same on every run and device).
  * Constraints: K % 32 == 0; scale_group == K or a power of two >= 32
- * dividing K; 1 <= sample <= 2^24; iters <= 1000; min(rows_per_cb, M) * K / 2
- * < 2^32 and ceil(M / rows_per_cb) <= 65535 (else KQ_EUNSUPPORTED).
+ * dividing K; 1 <= sample <= 2^24; iters <= 1000; K <= 2^18,
+ * min(rows_per_cb, M) * K / 2 < 2^32 and ceil(M / rows_per_cb) <= 65535
+ * (else KQ_EUNSUPPORTED).
  * ws: kq_vq_quantize_workspace_size bytes, 256-byte aligned (the scales,
  * the sample, the centroids and their sums); 0 means invalid arguments.
  * Launches: 3 + 2 * iters.

@@ -313,6 +313,7 @@ namespace {
 kq_status check_vq_quant(uint32_t M, uint32_t K, uint32_t rows_per_cb, uint32_t scale_group,
                          uint32_t sample) {
     if (M == 0 || K == 0 || K % 32 || rows_per_cb == 0) return KQ_EINVAL;
+    if (K > (1u << 18)) return KQ_EUNSUPPORTED;  // chunk maxima of a row are staged in LDS
     if (!(scale_group == K || (scale_group >= 32 && (scale_group & (scale_group - 1)) == 0 &&
                                K % scale_group == 0)))
         return KQ_EINVAL;

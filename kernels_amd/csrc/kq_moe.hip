@@ -121,7 +121,7 @@ __device__ __forceinline__ void unpack8(const Raw8<F32>& r, float v[8]) {
 // workgroups of the same launch (device-coherent loads); otherwise from an
 // earlier launch (plain loads).
 template <bool COHERENT>
-__device__ void topk_wave(const float* L, uint32_t NE, uint32_t TK,
+__device__ __forceinline__ void topk_wave(const float* L, uint32_t NE, uint32_t TK,
                           uint32_t* idx_out, float* wgt_out) {
     const uint32_t lane = threadIdx.x & 63;
     float v[4];
@@ -424,7 +424,7 @@ __device__ void get_plan(const Plan* plan_g, const uint32_t* idx, const float* w
 // at one token the top-k experts are distinct and slot s is plan entry s.
 // At most kPlanSlots slots (the launcher's limit), lane s takes slot s.
 constexpr uint32_t kPlanSlots = 2 * kMaxTopK;
-__device__ void plan_from_logits(const float* lg, uint32_t batch, uint32_t NE, uint32_t TK,
+__device__ __forceinline__ void plan_from_logits(const float* lg, uint32_t batch, uint32_t NE, uint32_t TK,
                                  Plan& ps, uint32_t* s_idx, float* s_wgt) {
     const uint32_t lane = threadIdx.x & 63;
     for (uint32_t t = 0; t < batch; ++t)

@@ -123,23 +123,29 @@ __device__ __forceinline__ void vq_load_cent(const float2* cent, uint32_t b, flo
     }
 }
 
+// One workgroup per row: the maxima of the row's 32-element chunks (thread
+// per chunk) into LDS, then per scale group the maximum of its chunks.
 template <int DT>
-__global__ __launch_bounds__(kQT) void vq_scale_k(const void* __restrict__ W, uint32_t M,
-                                                  uint32_t K, uint32_t G,
-                                                  uint16_t* __restrict__ S,
+__global__ __launch_bounds__(kQT) void vq_scale_k(const void* __restrict__ W, uint32_t K,
+                                                  uint32_t G, uint16_t* __restrict__ S,
                                                   float* __restrict__ sc) {
-    const size_t gi = (size_t)blockIdx.x * kQT + threadIdx.x;
-    if (gi >= (size_t)M * (K / G)) return;
-    const size_t base = gi * G;  // groups of a row are contiguous
-    float a = 0.0f;
-    for (uint32_t k = 0; k < G; k += 4) {
-        a = fmaxf(a, fabsf(wload<DT>(W, base + k)));
-        a = fmaxf(a, fabsf(wload<DT>(W, base + k + 1)));
-        a = fmaxf(a, fabsf(wload<DT>(W, base + k + 2)));
-        a = fmaxf(a, fabsf(wload<DT>(W, base + k + 3)));
+    extern __shared__ float cm[];  // [K / 32]
+    const uint32_t m = blockIdx.x, nck = K / 32, gpr = K / G;
+    const size_t row = (size_t)m * K;
+    for (uint32_t c = threadIdx.x; c < nck; c += kQT) {
+        float a = 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < 32; ++k) a = fmaxf(a, fabsf(wload<DT>(W, row + c * 32 + k)));
+        cm[c] = a;
     }
-    S[gi] = f2h(a);
-    sc[gi] = a > 0.0f ? a : 1.0f;
+    __syncthreads();
+    const uint32_t cpg = G / 32;
+    for (uint32_t g = threadIdx.x; g < gpr; g += kQT) {
+        float a = 0.0f;
+        for (uint32_t c = 0; c < cpg; ++c) a = fmaxf(a, cm[g * cpg + c]);
+        S[(size_t)m * gpr + g] = f2h(a);
+        sc[(size_t)m * gpr + g] = a > 0.0f ? a : 1.0f;
+    }
 }
 
 template <int DT>
@@ -252,8 +258,7 @@ hipError_t vq_quant_go(const void* W, uint32_t M, uint32_t K, uint32_t G, uint32
     float2* cent = reinterpret_cast<float2*>(ws + L.cent);
     VqAcc* acc = reinterpret_cast<VqAcc*>(ws + L.acc);
     const uint32_t nblk = (M + R - 1) / R;
-    const size_t ngr = (size_t)M * (K / G);
-    vq_scale_k<DT><<<(unsigned)((ngr + kQT - 1) / kQT), kQT, 0, s>>>(W, M, K, G, S, sc);
+    vq_scale_k<DT><<<M, kQT, (K / 32) * sizeof(float), s>>>(W, K, G, S, sc);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     vq_sample_k<DT><<<dim3((L.ns + kQT - 1) / kQT, nblk), kQT, 0, s>>>(
