@@ -189,8 +189,9 @@ typedef struct kq_moe_desc {
 void kq_moe_default_desc(kq_moe_desc* d);
 
 /* Bytes of workspace the MoE entry points need for `batch` tokens: the router
- * logits, a completion counter and the routing plan (distinct experts and
- * their token slots) that the block's gate/up and down kernels read. A new
+ * logits, a completion counter, the routing plan (distinct experts and
+ * their token slots) that the block's gate/up and down kernels read, and the
+ * per-slot down products of the block at 6 or more tokens. A new
  * workspace must be zeroed once with kq_moe_workspace_init (a kernel, not a
  * memset, so it can sit in a captured graph) before its first use; every call
  * leaves it ready for the next. Calls sharing one workspace must be
@@ -232,8 +233,10 @@ kq_status kq_moe_down_combine(const uint8_t* pool, const kq_moe_desc* d,
                               void* ws, size_t ws_bytes, kq_stream_t stream);
 
 /* The three passes back to back on one stream (encodeFused,
- * moe-fused/src/main.mm:176-206). idx, wgt, xh (if X is fp32) and H are
- * caller-provided outputs/intermediates of the sizes above. */
+ * moe-fused/src/main.mm:176-206): three launches; from 6 tokens down writes
+ * per-slot products to the workspace and a fourth, small launch sums them in
+ * slot order. idx, wgt, xh (if X is fp32) and H are caller-provided
+ * outputs/intermediates of the sizes above. */
 kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d,
                        const void* R, kq_dtype r_dtype, const void* X, kq_dtype x_dtype,
                        uint32_t batch, uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H,

@@ -27,6 +27,11 @@
 //    - per tile (moe_gate_up_k, moe_down_k; larger batches): a grid of
 //      (16-row tile, expert) or 8-output-row workgroups that issue all of
 //      their loads in one round trip.
+//    - expert-partitioned down (moe_dn_part_k, in the block from 6 tokens,
+//      where the slots' h vectors no longer fit one workgroup's LDS): a
+//      workgroup streams a row chunk of one expert with only that expert's h
+//      vectors in LDS and writes per-slot products to the workspace; a small
+//      moe_combine_k launch sums them in slot order (4 launches in all).
 //    Either way each selected expert's rows are read once per call for all
 //    token slots that chose it; a half-wave owns one row of a pair (gate /
 //    up, or two down rows; K = 2880 = 90 chunks -> 3 per lane), so SwiGLU
@@ -62,18 +67,20 @@ struct Plan {
     uint64_t mask[kMaxSlots][2];  // slot s: bit s of mask[.][0] (s < 64) or bit s-64 of [1]
 };
 
-// Workspace: [logits f32 batch x n_experts][completion counter][plan]
 struct WsLayout {
-    size_t lg, cnt, plan, total;
+    size_t lg, cnt, plan, ys, total;
 };
 
+// Workspace: [logits f32 batch x n_experts][completion counter][plan]
+// [per-slot down products f32 batch x top_k x hidden]
 WsLayout ws_layout(const kq_moe_desc& d, uint32_t batch) {
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
     WsLayout L;
     L.lg = 0;
     L.cnt = al(4ull * batch * d.n_experts);
     L.plan = L.cnt + 256;
-    L.total = al(L.plan + sizeof(Plan));
+    L.ys = al(L.plan + sizeof(Plan));
+    L.total = L.ys + al(4ull * batch * d.top_k * d.hidden);
     return L;
 }
 
@@ -1024,6 +1031,143 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
     }
 }
 
+// Down + weighted products, partitioned by expert (from 6 tokens, where the
+// slots' h vectors no longer fit one workgroup's LDS): workgroup (c, u)
+// streams row pairs [c * pp, (c + 1) * pp) of the plan's u-th expert with
+// only that expert's h vectors in LDS (one per slot that chose it, at most
+// one per token), and writes wgt_s * (down . h_s + bias) for each of those
+// slots s to ys[s][*]. moe_combine_k then sums each token's slots in k
+// order, as the reference's combine does (moe-fused/src/kernels.metal:254-263).
+// (Combining in the last workgroup of each row chunk instead measured slower:
+// 125 us per block at 8 tokens with device-coherent stores, 130 with fences,
+// against 119 with the separate launch.)
+template <int J>
+__global__ __launch_bounds__(64 * kStWaves) void moe_dn_part_k(
+    const uint8_t* __restrict__ pool, kq_moe_desc d, const float* __restrict__ wgt,
+    const Plan* __restrict__ plan_g, const uint16_t* __restrict__ H, uint32_t nslots,
+    float* __restrict__ ys, uint32_t pp) {
+    extern __shared__ __align__(16) unsigned char act[];  // [nvec h blocks]
+    const uint32_t HID = d.hidden, K = d.inter, nw = K >> 3, nch = K >> 5;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t half = lane >> 5, rowb = K >> 1, metab = (K >> 6) * 2;
+    const uint32_t u = blockIdx.y;
+    if (u >= plan_g->n) return;  // uniform: fewer distinct experts than slots
+    const uint32_t ex = min(plan_g->expert[u], d.n_experts - 1);
+    const uint64_t mk0 = plan_g->mask[u][0], mk1 = plan_g->mask[u][1];
+    const uint32_t nvec = __popcll(mk0) + __popcll(mk1);
+    const uint32_t npairs = HID >> 1, p0 = blockIdx.x * pp;
+    const uint32_t np = p0 < npairs ? min(pp, npairs - p0) : 0;
+    const uint32_t nit = np > wave ? (np - wave + kStWaves - 1) / kStWaves : 0;
+
+    // 1. the expert's h vectors, slot order: word tid of vector k (K <= 4096: nw <= threads)
+    const rsrc_t rh = make_rsrc(H, nslots * K * 2);
+    u32x4 sv[kStXr];
+    {
+        uint64_t a = mk0, b = mk1;
+#pragma unroll
+        for (int k = 0; k < kStXr; ++k) {
+            if ((uint32_t)k < nvec) {  // uniform
+                const uint32_t sl = pop_slot(a, b);
+                sv[k] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rh, tid < nw ? tid * 16 : kStOOB, __builtin_amdgcn_readfirstlane(sl * K * 2), 0);
+            }
+        }
+    }
+    // 2. prime the ring: row pairs p0 + wave, + kStWaves, ... of one expert
+    const StLane<J> L = st_lane<J>(d.off_down, d, K, half * rowb, half * metab, half * 2);
+    const rsrc_t r = make_rsrc(pool + (size_t)ex * d.blob, (uint32_t)d.blob);
+    constexpr int D = 2;
+    StSlot<J> ring[D];
+    uint32_t nis = 0;
+    auto issue = [&](StSlot<J>& e) __attribute__((always_inline)) {
+        const uint32_t it = min(nis, nit - 1);  // padding re-reads the last item
+        const uint32_t pr = p0 + wave + it * kStWaves;
+        st_issue<J>(e, r, L, 2 * pr * rowb, 2 * pr * metab, 2 * pr * 2);
+        ++nis;
+    };
+    if (nit > 0) {
+#pragma unroll
+        for (int q = 0; q < D; ++q) {
+            issue(ring[q]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // 3. staging store: permuted pairs and chunk constants, chunks past K zero
+#pragma unroll
+    for (int k = 0; k < kStXr; ++k) {
+        if ((uint32_t)k < nvec) {  // uniform
+            float cs, cc;
+            word_consts(sv[k], cs, cc);
+            cs = quad_sum(cs);
+            cc = quad_sum(cc);
+            if (tid < nw) {
+                const uint32_t ch = tid >> 2, jw = tid & 3;
+                unsigned char* blk = act + (k * J + (ch >> 5)) * kABlk;
+                *reinterpret_cast<u32x4*>(blk + jw * 512 + (ch & 31) * 16) = pair_perm(sv[k]);
+                if (jw == 0)
+                    *reinterpret_cast<float2*>(blk + 2048 + (ch & 31) * 8) = make_float2(cs, cc);
+            }
+        }
+    }
+    const uint32_t npad = 32 * J - nch;
+    for (uint32_t i = tid; i < nvec * 5 * npad; i += blockDim.x) {
+        const uint32_t v = i / (5 * npad), rem = i - v * 5 * npad, jw = rem / npad;
+        const uint32_t ch = nch + (rem - jw * npad);
+        unsigned char* blk = act + (v * J + (ch >> 5)) * kABlk;
+        if (jw < 4) *reinterpret_cast<u32x4*>(blk + jw * 512 + (ch & 31) * 16) = u32x4{0, 0, 0, 0};
+        else *reinterpret_cast<float2*>(blk + 2048 + (ch & 31) * 8) = make_float2(0.0f, 0.0f);
+    }
+    __syncthreads();
+
+    // 4. stream
+    const DequantConsts kc;
+    auto step = [&](const StSlot<J>& e, uint32_t it) __attribute__((always_inline)) {
+        if (it >= nit) return;  // padding (uniform)
+        const uint32_t pr = p0 + wave + it * kStWaves;
+        StDq<J> q;
+        st_dequant<J>(e, kc, q);
+        const float b0 = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 0));
+        const float b1 = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 32));
+        uint64_t a = mk0, b = mk1;
+        for (uint32_t k = 0; k < nvec; ++k) {
+            const uint32_t sl = pop_slot(a, b);
+            const float2 hs = half_sums(st_dot<J>(q, act, k));
+            const float wt = wgt[sl];
+            if (lane == 0) {
+                ys[(size_t)sl * HID + 2 * pr] = wt * (hs.x + b0);
+                ys[(size_t)sl * HID + 2 * pr + 1] = wt * (hs.y + b1);
+            }
+        }
+    };
+    if (nit > 0) {
+        const uint32_t nsteps = (nit + D - 1) / D * D;
+        uint32_t it = 0;
+        for (; it + D < nsteps; it += D) {
+#pragma unroll
+            for (int q = 0; q < D; ++q) {
+                step(ring[q], it + q);
+                issue(ring[q]);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < D; ++q) step(ring[q], it + q);
+    }
+}
+
+// Y[t][m] = sum over k of ys[t * TK + k][m], in k order.
+__global__ __launch_bounds__(256) void moe_combine_k(const float* __restrict__ ys, void* Y,
+                                                     int y_f32, uint32_t batch, uint32_t TK,
+                                                     uint32_t HID) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= batch * HID) return;
+    const uint32_t t = i / HID, m = i - t * HID;
+    float acc = 0.0f;
+    for (uint32_t q = 0; q < TK; ++q) acc += ys[(size_t)(t * TK + q) * HID + m];
+    if (y_f32) reinterpret_cast<float*>(Y)[i] = acc;
+    else reinterpret_cast<uint16_t*>(Y)[i] = f2h(acc);
+}
+
 __global__ void fill_zero_k(uint32_t* p, size_t n) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
         p[i] = 0u;
@@ -1169,12 +1313,53 @@ hipError_t launch_gu(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* 
     }
 }
 
+// Row chunks: about two workgroups per CU over the plan's experts (measured
+// at 8 tokens: 119.4 us per block against 123.1 with one and 122.6 with four).
+template <int J>
+hipError_t go_dn_part(const uint8_t* pool, const kq_moe_desc& d, const float* wgt,
+                      const Plan* plan, const uint16_t* H, void* Y, bool y_f32, uint32_t batch,
+                      float* ys, hipStream_t s) {
+    auto kern = moe_dn_part_k<J>;
+    const uint32_t nslots = batch * d.top_k, npairs = d.hidden / 2;
+    const uint32_t nu = nslots < d.n_experts ? nslots : d.n_experts;  // plan entries at most
+    const uint32_t nchunk = 2 * cu_count() / nu > 0 ? 2 * cu_count() / nu : 1;
+    const uint32_t pp = (npairs + nchunk - 1) / nchunk;
+    const size_t lds = st_act_bytes(batch, d.inter);  // at most one slot per token per expert
+    hipError_t e = st_lds(kern, lds);
+    if (e != hipSuccess) return e;
+    kern<<<dim3((npairs + pp - 1) / pp, nu), 64 * kStWaves, lds, s>>>(pool, d, wgt, plan, H,
+                                                                       nslots, ys, pp);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const uint32_t n = batch * d.hidden;
+    moe_combine_k<<<(n + 255) / 256, 256, 0, s>>>(ys, Y, y_f32 ? 1 : 0, batch, d.top_k, d.hidden);
+    return hipGetLastError();
+}
+
+// The expert-partitioned down: up to kStXr tokens (the h vectors a thread
+// stages), inter <= one word per thread, the h blocks in LDS.
+bool dn_part_ok(const kq_moe_desc& d, uint32_t batch) {
+    return batch <= (uint32_t)kStXr && (d.inter >> 3) <= 64u * kStWaves &&
+           d.blob < (1ull << 31) && st_act_bytes(batch, d.inter) + 1024 <= kLdsMax;
+}
+
+// ys: workspace for the per-slot products (nullptr: not available).
 template <bool FP>
 hipError_t launch_dn(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
                      const float* wgt, const Plan* plan, const uint16_t* H, void* Y, bool y_f32,
-                     uint32_t batch, hipStream_t s) {
+                     uint32_t batch, hipStream_t s, float* ys = nullptr) {
     const uint32_t nslots = batch * d.top_k, npairs = d.hidden / 2;
     const uint32_t pp = (npairs + cu_count() - 1) / cu_count();
+    if constexpr (FP) {
+        if (ys && !st_ok(d, nslots, d.inter, (size_t)nslots * 2 * pp * 4) && dn_part_ok(d, batch)) {
+            switch (chunks_j(d.inter)) {
+                case 1: return go_dn_part<1>(pool, d, wgt, plan, H, Y, y_f32, batch, ys, s);
+                case 2: return go_dn_part<2>(pool, d, wgt, plan, H, Y, y_f32, batch, ys, s);
+                case 3: return go_dn_part<3>(pool, d, wgt, plan, H, Y, y_f32, batch, ys, s);
+                case 4: return go_dn_part<4>(pool, d, wgt, plan, H, Y, y_f32, batch, ys, s);
+                default: return hipErrorInvalidValue;
+            }
+        }
+    }
     if (st_ok(d, nslots, d.inter, (size_t)nslots * 2 * pp * 4)) {
         switch (chunks_j(d.inter)) {
             case 1: return go_dn_st<1, FP>(pool, d, idx, wgt, plan, H, Y, y_f32, batch, pp, s);
@@ -1259,7 +1444,8 @@ hipError_t launch_moe_block(const uint8_t* pool, const kq_moe_desc& d, const voi
         e = launch_gu<true>(pool, d, idx, plan, xin, H, batch, s);
     }
     if (e != hipSuccess) return e;
-    return launch_dn<true>(pool, d, idx, wgt, plan, H, Y, y_f32, batch, s);
+    return launch_dn<true>(pool, d, idx, wgt, plan, H, Y, y_f32, batch, s,
+                           reinterpret_cast<float*>(w + L.ys));
 }
 
 }  // namespace kq

@@ -195,6 +195,30 @@ def test_block_full_pool(gpu, batch):
     del pool
 
 
+@pytest.mark.parametrize("batch", [6, 16])
+def test_block_expert_partitioned_down(gpu, pool16, batch):
+    """From 6 tokens the slots' h vectors no longer fit one workgroup's LDS:
+    down runs partitioned by expert (per-slot products to the workspace, then
+    the combine launch). 16 experts, top-4: at 16 tokens every expert is
+    chosen by several tokens."""
+    host, pool = pool16
+    d = _pool_desc(16)
+    R, X = gen.moe_inputs(16, batch=batch, seed=40 + batch)
+    oidx, owgt, lg = oracle.moe_router(R, oracle.F16, X, oracle.F16, batch, odesc(d))
+    assert routing_margin(lg, 4) > 1e-5
+    _, _, Yref = oracle.moe_block(host, odesc(d), R, oracle.F16, X, oracle.F16, batch)
+    b = Block(gpu, d, batch)
+    Rd, Xd = dev(R, gpu).view(torch.float16), dev(X, gpu).view(torch.float16)
+    for rep in range(2):
+        b.y.fill_(float("nan"))
+        kq.moe_block(pool, d, Rd, Xd, b.idx, b.wgt, b.H, b.y, b.ws, b.wsb, batch=batch)
+        torch.cuda.synchronize()
+        assert np.array_equal(b.idx.cpu().numpy().astype(np.uint32), oidx)
+        got = to_f64(b.y)
+        assert_close(got, Yref, what=f"block batch {batch} rep {rep}")
+        assert inf_rel(got, Yref) < 2e-3
+
+
 def test_block_fp32_inputs_and_fp16_out(gpu, pool16):
     """Reference-fidelity inputs: fp32 router and x (xh written by the router)."""
     host, pool = pool16
@@ -216,7 +240,7 @@ def test_block_fp32_inputs_and_fp16_out(gpu, pool16):
     assert_close(got, Yref, atol=2e-2, rtol=2e-3, what="fp32-in block")
 
 
-@pytest.mark.parametrize("batch", [1, 8])
+@pytest.mark.parametrize("batch", [1, 8, 16])
 def test_block_graph_replays(gpu, pool16, batch):
     """The block captured in a HIP graph: every replay (with eager block calls
     and synchronisations between replays, and the router's completion counter
