@@ -27,6 +27,9 @@
 //    - per tile (moe_gate_up_k, moe_down_k; larger batches): a grid of
 //      (16-row tile, expert) or 8-output-row workgroups that issue all of
 //      their loads in one round trip.
+//    - expert-partitioned gate/up (moe_gu_part_k, in the block from 3
+//      tokens): a workgroup streams a row chunk of one expert's gate and up
+//      rows with only the x vectors of that expert's tokens in LDS;
 //    - expert-partitioned down (moe_dn_part_k, in the block from 6 tokens,
 //      where the slots' h vectors no longer fit one workgroup's LDS): a
 //      workgroup streams a row chunk of one expert with only that expert's h
@@ -1031,6 +1034,120 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
     }
 }
 
+// Gate/up + SwiGLU, partitioned by expert (3-16 tokens; about two workgroups
+// per CU -- at 8 tokens 116.3 us per block against 130.3 with one and 118.4
+// with four; the per-tile kernel gave 119.0): workgroup (c, u)
+// streams rows [c * rp, (c + 1) * rp) of the plan's u-th expert (half 0 the
+// gate row, half 1 the up row) with only the x vectors of that expert's
+// tokens in LDS, and writes h for each of its slots. Each expert's rows are
+// read once for all its slots, as in the other forms.
+template <int J>
+__global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
+    const uint8_t* __restrict__ pool, kq_moe_desc d, const Plan* __restrict__ plan_g,
+    const uint16_t* __restrict__ xh, uint32_t batch, uint16_t* __restrict__ H, uint32_t rp) {
+    extern __shared__ __align__(16) unsigned char act[];  // [nvec x blocks]
+    const uint32_t K = d.hidden, IN = d.inter, TK = d.top_k, nw = K >> 3, nch = K >> 5;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t half = lane >> 5, rowb = K >> 1, metab = (K >> 6) * 2;
+    const uint32_t u = blockIdx.y;
+    if (u >= plan_g->n) return;  // uniform: fewer distinct experts than slots
+    const uint32_t ex = min(plan_g->expert[u], d.n_experts - 1);
+    const uint64_t mk0 = plan_g->mask[u][0], mk1 = plan_g->mask[u][1];
+    const uint32_t nvec = __popcll(mk0) + __popcll(mk1);
+    const uint32_t i0 = blockIdx.x * rp, ni = i0 < IN ? min(rp, IN - i0) : 0;
+    const uint32_t nit = ni > wave ? (ni - wave + kStWaves - 1) / kStWaves : 0;
+
+    // 1. x of the expert's tokens, slot order: word tid of vector k (K <= 4096: nw <= threads)
+    const rsrc_t rx = make_rsrc(xh, batch * K * 2);
+    u32x4 sv[kStXr];
+    {
+        uint64_t a = mk0, b = mk1;
+#pragma unroll
+        for (int k = 0; k < kStXr; ++k) {
+            if ((uint32_t)k < nvec) {  // uniform
+                const uint32_t tok = pop_slot(a, b) / TK;
+                sv[k] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rx, tid < nw ? tid * 16 : kStOOB, __builtin_amdgcn_readfirstlane(tok * K * 2), 0);
+            }
+        }
+    }
+    // 2. prime the ring: rows i0 + wave, + kStWaves, ... of one expert
+    const StLane<J> L = st_lane<J>(half ? d.off_up : d.off_gate, d, K, 0, 0, 0);
+    const rsrc_t r = make_rsrc(pool + (size_t)ex * d.blob, (uint32_t)d.blob);
+    constexpr int D = 2;
+    StSlot<J> ring[D];
+    uint32_t nis = 0;
+    auto issue = [&](StSlot<J>& e) __attribute__((always_inline)) {
+        const uint32_t it = min(nis, nit - 1);  // padding re-reads the last item
+        const uint32_t i = i0 + wave + it * kStWaves;
+        st_issue<J>(e, r, L, i * rowb, i * metab, i * 2);
+        ++nis;
+    };
+    if (nit > 0) {
+#pragma unroll
+        for (int q = 0; q < D; ++q) {
+            issue(ring[q]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // 3. staging store: permuted pairs and chunk constants, chunks past K zero
+#pragma unroll
+    for (int k = 0; k < kStXr; ++k) {
+        if ((uint32_t)k < nvec) {  // uniform
+            float cs, cc;
+            word_consts(sv[k], cs, cc);
+            cs = quad_sum(cs);
+            cc = quad_sum(cc);
+            if (tid < nw) {
+                const uint32_t ch = tid >> 2, jw = tid & 3;
+                unsigned char* blk = act + (k * J + (ch >> 5)) * kABlk;
+                *reinterpret_cast<u32x4*>(blk + jw * 512 + (ch & 31) * 16) = pair_perm(sv[k]);
+                if (jw == 0)
+                    *reinterpret_cast<float2*>(blk + 2048 + (ch & 31) * 8) = make_float2(cs, cc);
+            }
+        }
+    }
+    const uint32_t npad = 32 * J - nch;
+    for (uint32_t i = tid; i < nvec * 5 * npad; i += blockDim.x) {
+        const uint32_t v = i / (5 * npad), rem = i - v * 5 * npad, jw = rem / npad;
+        const uint32_t ch = nch + (rem - jw * npad);
+        unsigned char* blk = act + (v * J + (ch >> 5)) * kABlk;
+        if (jw < 4) *reinterpret_cast<u32x4*>(blk + jw * 512 + (ch & 31) * 16) = u32x4{0, 0, 0, 0};
+        else *reinterpret_cast<float2*>(blk + 2048 + (ch & 31) * 8) = make_float2(0.0f, 0.0f);
+    }
+    __syncthreads();
+    if (nit == 0) return;  // no later barrier
+
+    // 4. stream
+    const DequantConsts kc;
+    auto step = [&](const StSlot<J>& e, uint32_t it) __attribute__((always_inline)) {
+        if (it >= nit) return;  // padding (uniform)
+        const uint32_t i = i0 + wave + it * kStWaves;
+        StDq<J> q;
+        st_dequant<J>(e, kc, q);
+        const float bg = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 0));
+        const float bu = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 32));
+        uint64_t a = mk0, b = mk1;
+        for (uint32_t k = 0; k < nvec; ++k) {
+            const uint32_t sl = pop_slot(a, b);
+            const float2 hs = half_sums(st_dot<J>(q, act, k));
+            if (lane == 0) H[(size_t)sl * IN + i] = f2h(swiglu(hs.x + bg, hs.y + bu));
+        }
+    };
+    const uint32_t nsteps = (nit + D - 1) / D * D;
+    uint32_t it = 0;
+    for (; it + D < nsteps; it += D) {
+#pragma unroll
+        for (int q = 0; q < D; ++q) {
+            step(ring[q], it + q);
+            issue(ring[q]);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < D; ++q) step(ring[q], it + q);
+}
+
 // Down + weighted products, partitioned by expert (from 6 tokens, where the
 // slots' h vectors no longer fit one workgroup's LDS): workgroup (c, u)
 // streams row pairs [c * pp, (c + 1) * pp) of the plan's u-th expert with
@@ -1298,12 +1415,46 @@ hipError_t launch_gu_st(const uint8_t* pool, const kq_moe_desc& d, const uint32_
     }
 }
 
+template <int J>
+hipError_t go_gu_part(const uint8_t* pool, const kq_moe_desc& d, const Plan* plan,
+                      const uint16_t* xh, uint16_t* H, uint32_t batch, hipStream_t s) {
+    auto kern = moe_gu_part_k<J>;
+    const uint32_t nslots = batch * d.top_k;
+    const uint32_t nu = nslots < d.n_experts ? nslots : d.n_experts;  // plan entries at most
+    const uint32_t nchunk = 2 * cu_count() / nu > 0 ? 2 * cu_count() / nu : 1;
+    const uint32_t rp = (d.inter + nchunk - 1) / nchunk;
+    const size_t lds = st_act_bytes(batch, d.hidden);  // at most one slot per token per expert
+    const hipError_t e = st_lds(kern, lds);
+    if (e != hipSuccess) return e;
+    kern<<<dim3((d.inter + rp - 1) / rp, nu), 64 * kStWaves, lds, s>>>(pool, d, plan, xh, batch, H,
+                                                                        rp);
+    return hipGetLastError();
+}
+
+// The expert-partitioned gate/up: up to kStXr tokens, hidden <= one word per
+// thread, the x blocks in LDS.
+bool gu_part_ok(const kq_moe_desc& d, uint32_t batch) {
+    return batch <= (uint32_t)kStXr && (d.hidden >> 3) <= 64u * kStWaves &&
+           d.blob < (1ull << 31) && st_act_bytes(batch, d.hidden) + 1024 <= kLdsMax;
+}
+
 template <bool FP>
 hipError_t launch_gu(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
                      const Plan* plan, const uint16_t* xh, uint16_t* H, uint32_t batch,
                      hipStream_t s) {
     if (gu_streams(d, batch))
         return launch_gu_st<FP ? 1 : 0>(pool, d, idx, plan, xh, H, batch, GuTopk{}, s);
+    if constexpr (FP) {  // the plan is in the workspace
+        if (gu_part_ok(d, batch)) {
+            switch (chunks_j(d.hidden)) {
+                case 1: return go_gu_part<1>(pool, d, plan, xh, H, batch, s);
+                case 2: return go_gu_part<2>(pool, d, plan, xh, H, batch, s);
+                case 3: return go_gu_part<3>(pool, d, plan, xh, H, batch, s);
+                case 4: return go_gu_part<4>(pool, d, plan, xh, H, batch, s);
+                default: return hipErrorInvalidValue;
+            }
+        }
+    }
     switch (chunks_j(d.hidden)) {
         case 1: return go_gu<1, FP>(pool, d, idx, plan, xh, H, batch, s);
         case 2: return go_gu<2, FP>(pool, d, idx, plan, xh, H, batch, s);
