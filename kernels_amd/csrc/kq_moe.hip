@@ -17,30 +17,29 @@
 //    wave of the streaming gate/up launch runs the top-k and builds the plan
 //    itself (no barrier before its weight loads), and workgroup 0 publishes
 //    idx, wgt and the plan for down.
-// 2. gate/up + SwiGLU, and 3. down + weighted combine, each in one of two
-//    forms:
+// 2. gate/up + SwiGLU, and 3. down + weighted combine, in these forms:
 //    - streaming (moe_gu_stream_k up to 2 tokens, moe_dn_stream_k while the
-//      slots' h vectors fit in LDS): one workgroup per CU, each wave streams
-//      (expert, row pair) items through a 2-deep ring of register slots,
-//      compute overlapped with the next item's loads; the activations are
-//      prepared once per workgroup in LDS (at one token, held in registers);
-//    - per tile (moe_gate_up_k, moe_down_k; larger batches): a grid of
+//      slots' h vectors fit in LDS, up to 5 tokens at gpt-oss shapes): one
+//      workgroup per CU, each wave streams (expert, row pair) items through
+//      a 2-deep ring of register slots, compute overlapped with the next
+//      item's loads; the activations are prepared once per workgroup in LDS
+//      (at one token, held in registers); down keeps per-slot
+//      wgt * (down . h + bias) in LDS and sums the slots in k order;
+//    - expert-partitioned (the block's gate/up from 3 tokens, moe_gu_part_k;
+//      its down from 6 tokens, moe_dn_part_k): workgroup (row chunk, plan
+//      entry) streams one expert's rows with only that expert's
+//      activations in LDS; down writes per-slot products to the workspace
+//      and a small moe_combine_k launch sums them in slot order (4
+//      launches in all);
+//    - per tile (moe_gate_up_k, moe_down_k): the standalone entry points
+//      past the streaming limits (they take no workspace): a grid of
 //      (16-row tile, expert) or 8-output-row workgroups that issue all of
 //      their loads in one round trip.
-//    - expert-partitioned gate/up (moe_gu_part_k, in the block from 3
-//      tokens): a workgroup streams a row chunk of one expert's gate and up
-//      rows with only the x vectors of that expert's tokens in LDS;
-//    - expert-partitioned down (moe_dn_part_k, in the block from 6 tokens,
-//      where the slots' h vectors no longer fit one workgroup's LDS): a
-//      workgroup streams a row chunk of one expert with only that expert's h
-//      vectors in LDS and writes per-slot products to the workspace; a small
-//      moe_combine_k launch sums them in slot order (4 launches in all).
-//    Either way each selected expert's rows are read once per call for all
+//    Every form reads each selected expert's rows once per call for all
 //    token slots that chose it; a half-wave owns one row of a pair (gate /
 //    up, or two down rows; K = 2880 = 90 chunks -> 3 per lane), so SwiGLU
-//    and the combine see the two half sums. Down keeps per-slot
-//    wgt * (down . h + bias) in LDS and sums the slots in k order --
-//    deterministic, no atomics.
+//    and the combine see the two half sums. Sums are deterministic (fixed
+//    order, no atomics).
 //
 // Activations are used as permuted fp16 pairs with per-chunk sums (the
 // AND-OR dequant of kq_device.h); bf16 group scale and bias apply once per
