@@ -877,12 +877,12 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
         adv(ci);
         ++nis;
     };
-    if (nit > 0) {
+    // primed even without items (a valid row, unused): the same number of
+    // loads on every path lets the compiler wait for the staging loads alone
 #pragma unroll
-        for (int s = 0; s < D; ++s) {
-            issue(ring[s]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+    for (int s = 0; s < D; ++s) {
+        issue(ring[s]);
+        __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (SRC == 2) {
         if (blockIdx.x == 0) publish_plan(ps, s_idx, s_wgt, batch * TK, idx_out, wgt_out, plan_out);
@@ -978,12 +978,12 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
         adv(ci);
         ++nis;
     };
-    if (nit > 0) {
+    // primed even without items (a valid row pair, unused): the same number
+    // of loads on every path lets the compiler wait for the staging loads alone
 #pragma unroll
-        for (int s = 0; s < D; ++s) {
-            issue(ring[s]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+    for (int s = 0; s < D; ++s) {
+        issue(ring[s]);
+        __builtin_amdgcn_sched_barrier(0);
     }
     st_stage_store<J>(st, act, nslots, K);
     __syncthreads();
@@ -1078,17 +1078,17 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
     StSlot<J> ring[D];
     uint32_t nis = 0;
     auto issue = [&](StSlot<J>& e) __attribute__((always_inline)) {
-        const uint32_t it = min(nis, nit - 1);  // padding re-reads the last item
-        const uint32_t i = i0 + wave + it * kStWaves;
+        // padding re-reads the last item; a wave without items loads row i0
+        const uint32_t it = nit ? min(nis, nit - 1) : 0u;
+        const uint32_t i = nit ? i0 + wave + it * kStWaves : i0;
         st_issue<J>(e, r, L, i * rowb, i * metab, i * 2);
         ++nis;
     };
-    if (nit > 0) {
+    // primed on every path (same load count: the staging waits only for its own loads)
 #pragma unroll
-        for (int q = 0; q < D; ++q) {
-            issue(ring[q]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+    for (int q = 0; q < D; ++q) {
+        issue(ring[q]);
+        __builtin_amdgcn_sched_barrier(0);
     }
     // 3. staging store: permuted pairs and chunk constants, chunks past K zero
 #pragma unroll
@@ -1197,17 +1197,17 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_part_k(
     StSlot<J> ring[D];
     uint32_t nis = 0;
     auto issue = [&](StSlot<J>& e) __attribute__((always_inline)) {
-        const uint32_t it = min(nis, nit - 1);  // padding re-reads the last item
-        const uint32_t pr = p0 + wave + it * kStWaves;
+        // padding re-reads the last item; a wave without items loads pair p0
+        const uint32_t it = nit ? min(nis, nit - 1) : 0u;
+        const uint32_t pr = nit ? p0 + wave + it * kStWaves : p0;
         st_issue<J>(e, r, L, 2 * pr * rowb, 2 * pr * metab, 2 * pr * 2);
         ++nis;
     };
-    if (nit > 0) {
+    // primed on every path (same load count: the staging waits only for its own loads)
 #pragma unroll
-        for (int q = 0; q < D; ++q) {
-            issue(ring[q]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+    for (int q = 0; q < D; ++q) {
+        issue(ring[q]);
+        __builtin_amdgcn_sched_barrier(0);
     }
     // 3. staging store: permuted pairs and chunk constants, chunks past K zero
 #pragma unroll
