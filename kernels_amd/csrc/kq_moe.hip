@@ -894,21 +894,32 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     if constexpr (XREG) st_xload<J>(xr, act, 0);
 
     const DequantConsts kc;
-    auto step = [&](const StSlot<J>& e, uint32_t it) __attribute__((always_inline)) {
-        if (it >= nit) return;  // padding (uniform)
+    // One store per step, by every lane: lane j < the item's slot count writes
+    // slot j's h, the other lanes repeat the last slot's write. A fixed store
+    // count keeps the next ring wait from also waiting for this step's store.
+    // Steps of the main loop are never padding; only the tail checks.
+    auto step = [&](const StSlot<J>& e, uint32_t it, bool tail) __attribute__((always_inline)) {
+        if (tail && it >= nit) return;  // padding (uniform)
         uint64_t m0 = ps.mask[cc.u][0], m1 = ps.mask[cc.u][1];
         StDq<J> q;
         st_dequant<J>(e, kc, q);
         const float bg = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 0));
         const float bu = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 32));
-        while (m0 | m1) {
+        size_t oi = 0;
+        uint16_t ov = 0;
+        for (uint32_t k = 0; m0 | m1; ++k) {
             const uint32_t s = pop_slot(m0, m1);
             float acc;
             if constexpr (XREG) acc = st_dotx<J>(q, xr);
             else acc = st_dot<J>(q, act, s / TK);
             const float2 hs = half_sums(acc);
-            if (lane == 0) H[(size_t)s * IN + cc.i] = f2h(swiglu(hs.x + bg, hs.y + bu));
+            const uint16_t hv = f2h(swiglu(hs.x + bg, hs.y + bu));
+            if (lane >= k) {
+                oi = (size_t)s * IN + cc.i;
+                ov = hv;
+            }
         }
+        H[oi] = ov;
         adv(cc);
     };
     const uint32_t nsteps = (nit + D - 1) / D * D;
@@ -916,12 +927,12 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     for (; it + D < nsteps; it += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
-            step(ring[s], it + s);
+            step(ring[s], it + s, false);
             issue(ring[s]);
         }
     }
 #pragma unroll
-    for (int s = 0; s < D; ++s) step(ring[s], it + s);
+    for (int s = 0; s < D; ++s) step(ring[s], it + s, true);
 }
 
 // Down + weighted combine: workgroup w owns output row pairs [p0, p1) for
@@ -1120,31 +1131,41 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
 
     // 4. stream
     const DequantConsts kc;
-    auto step = [&](const StSlot<J>& e, uint32_t it) __attribute__((always_inline)) {
-        if (it >= nit) return;  // padding (uniform)
+    // One store per step by every lane (lane j < nvec: slot j; the rest repeat
+    // the last), so the next ring wait does not also wait for it; only the
+    // tail checks for padding.
+    auto step = [&](const StSlot<J>& e, uint32_t it, bool tail) __attribute__((always_inline)) {
+        if (tail && it >= nit) return;  // padding (uniform)
         const uint32_t i = i0 + wave + it * kStWaves;
         StDq<J> q;
         st_dequant<J>(e, kc, q);
         const float bg = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 0));
         const float bu = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 32));
         uint64_t a = mk0, b = mk1;
+        size_t oi = 0;
+        uint16_t ov = 0;
         for (uint32_t k = 0; k < nvec; ++k) {
             const uint32_t sl = pop_slot(a, b);
             const float2 hs = half_sums(st_dot<J>(q, act, k));
-            if (lane == 0) H[(size_t)sl * IN + i] = f2h(swiglu(hs.x + bg, hs.y + bu));
+            const uint16_t hv = f2h(swiglu(hs.x + bg, hs.y + bu));
+            if (lane >= k) {
+                oi = (size_t)sl * IN + i;
+                ov = hv;
+            }
         }
+        H[oi] = ov;
     };
     const uint32_t nsteps = (nit + D - 1) / D * D;
     uint32_t it = 0;
     for (; it + D < nsteps; it += D) {
 #pragma unroll
         for (int q = 0; q < D; ++q) {
-            step(ring[q], it + q);
+            step(ring[q], it + q, false);
             issue(ring[q]);
         }
     }
 #pragma unroll
-    for (int q = 0; q < D; ++q) step(ring[q], it + q);
+    for (int q = 0; q < D; ++q) step(ring[q], it + q, true);
 }
 
 // Down + weighted products, partitioned by expert (from 6 tokens, where the
@@ -1238,23 +1259,29 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_part_k(
 
     // 4. stream
     const DequantConsts kc;
-    auto step = [&](const StSlot<J>& e, uint32_t it) __attribute__((always_inline)) {
-        if (it >= nit) return;  // padding (uniform)
+    // One store per step by every lane: lane (h, j), j < nvec, writes slot j's
+    // row 2 pr + h; the other lanes repeat the last slot's. The next ring wait
+    // then does not also wait for it; only the tail checks for padding.
+    auto step = [&](const StSlot<J>& e, uint32_t it, bool tail) __attribute__((always_inline)) {
+        if (tail && it >= nit) return;  // padding (uniform)
         const uint32_t pr = p0 + wave + it * kStWaves;
         StDq<J> q;
         st_dequant<J>(e, kc, q);
         const float b0 = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 0));
         const float b1 = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 32));
         uint64_t a = mk0, b = mk1;
+        size_t oi = 0;
+        float ov = 0.0f;
         for (uint32_t k = 0; k < nvec; ++k) {
             const uint32_t sl = pop_slot(a, b);
             const float2 hs = half_sums(st_dot<J>(q, act, k));
             const float wt = wgt[sl];
-            if (lane == 0) {
-                ys[(size_t)sl * HID + 2 * pr] = wt * (hs.x + b0);
-                ys[(size_t)sl * HID + 2 * pr + 1] = wt * (hs.y + b1);
+            if ((lane & 31) >= k) {
+                oi = (size_t)sl * HID + 2 * pr + half;
+                ov = wt * (half ? hs.y + b1 : hs.x + b0);
             }
         }
+        ys[oi] = ov;
     };
     if (nit > 0) {
         const uint32_t nsteps = (nit + D - 1) / D * D;
@@ -1262,12 +1289,12 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_part_k(
         for (; it + D < nsteps; it += D) {
 #pragma unroll
             for (int q = 0; q < D; ++q) {
-                step(ring[q], it + q);
+                step(ring[q], it + q, false);
                 issue(ring[q]);
             }
         }
 #pragma unroll
-        for (int q = 0; q < D; ++q) step(ring[q], it + q);
+        for (int q = 0; q < D; ++q) step(ring[q], it + q, true);
     }
 }
 
