@@ -162,6 +162,13 @@ __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
     };
     x_load(0);
     __builtin_amdgcn_sched_barrier(0);
+    // With more than 8 waves, the later waves' staging loads would queue in
+    // the CU's load path behind the earlier waves' ring loads, and the
+    // staging barrier waits for the last of them. A barrier (no wait) puts
+    // every wave's staging loads first. Measured at 14336 x 4096 (14 waves):
+    // 8.41 -> 7.73 us; at 8 waves or fewer it costs more than it saves.
+    if (A.P * A.Q > 8) __builtin_amdgcn_s_barrier();  // uniform
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- 2. prime the ring
     // lane offsets: full steps, and the last step (OOB past the row's end)
