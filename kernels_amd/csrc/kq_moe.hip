@@ -957,8 +957,24 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
 
     StStage st;
     st_stage_load(st, H, nslots, K);
-    get_plan<FROM_PLAN>(plan_g, idx, wgt, nslots, d.n_experts, ps, s_idx, s_wgt, bits);
-    const uint32_t nexp = ps.n, npairs = HID >> 1;
+    // From the workspace plan, every wave reads the plan and the weights
+    // itself at uniform addresses (scalar loads): no LDS copy and no barrier,
+    // so the h staging loads stay in flight while the ring is primed.
+    if constexpr (!FROM_PLAN)
+        get_plan<false>(plan_g, idx, wgt, nslots, d.n_experts, ps, s_idx, s_wgt, bits);
+    auto p_expert = [&](uint32_t u) __attribute__((always_inline)) {
+        if constexpr (FROM_PLAN) return plan_g->expert[u];
+        else return ps.expert[u];
+    };
+    auto p_mask = [&](uint32_t u, int h) __attribute__((always_inline)) {
+        if constexpr (FROM_PLAN) return plan_g->mask[u][h];
+        else return ps.mask[u][h];
+    };
+    auto p_wgt = [&](uint32_t sl) __attribute__((always_inline)) {
+        if constexpr (FROM_PLAN) return wgt[sl];
+        else return s_wgt[sl];
+    };
+    const uint32_t nexp = FROM_PLAN ? plan_g->n : ps.n, npairs = HID >> 1;
     const uint32_t p0 = blockIdx.x * pp, np = p0 < npairs ? min(pp, npairs - p0) : 0;
     const uint32_t N = nexp * np;
     const uint32_t nit = N > wave ? (N - wave + kStWaves - 1) / kStWaves : 0;
@@ -982,7 +998,7 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
     auto issue = [&](StSlot<J>& e) __attribute__((always_inline)) {
         if (nis < nit) clast = ci;  // padding re-reads the last item
         const uint32_t ex =
-            __builtin_amdgcn_readfirstlane(min(ps.expert[min(clast.u, nexp - 1)], d.n_experts - 1));
+            __builtin_amdgcn_readfirstlane(min(p_expert(min(clast.u, nexp - 1)), d.n_experts - 1));
         const rsrc_t r = make_rsrc(pool + (size_t)ex * d.blob, (uint32_t)d.blob);
         const uint32_t p = __builtin_amdgcn_readfirstlane(clast.p);
         st_issue<J>(e, r, L, 2 * p * rowb, 2 * p * metab, 2 * p * 2);
@@ -1004,7 +1020,7 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
         if (it >= nit) return;  // padding (uniform)
         const Cur c = cc;
         adv(cc);
-        uint64_t m0 = ps.mask[c.u][0], m1 = ps.mask[c.u][1];
+        uint64_t m0 = p_mask(c.u, 0), m1 = p_mask(c.u, 1);
         StDq<J> q;
         st_dequant<J>(e, kc, q);
         const float b0 = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 0));
@@ -1013,7 +1029,7 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
         while (m0 | m1) {
             const uint32_t s = pop_slot(m0, m1);
             const float2 hs = half_sums(st_dot<J>(q, act, s));
-            const float wt = s_wgt[s];
+            const float wt = p_wgt(s);
             if (lane == 0) {
                 ys[s * 2 * pp + r] = wt * (hs.x + b0);
                 ys[s * 2 * pp + r + 1] = wt * (hs.y + b1);

@@ -195,12 +195,14 @@ def test_block_full_pool(gpu, batch):
     del pool
 
 
-@pytest.mark.parametrize("batch", [6, 16])
+@pytest.mark.parametrize("batch", [3, 5, 6, 16])
 def test_block_expert_partitioned_down(gpu, pool16, batch):
-    """From 6 tokens the slots' h vectors no longer fit one workgroup's LDS:
-    down runs partitioned by expert (per-slot products to the workspace, then
-    the combine launch). 16 experts, top-4: at 16 tokens every expert is
-    chosen by several tokens."""
+    """From 3 tokens gate/up runs partitioned by expert. At 3-5 tokens the
+    streaming down reads the plan and weights from the workspace; from 6
+    tokens the slots' h vectors no longer fit one workgroup's LDS, so down
+    runs partitioned by expert too (per-slot products to the workspace, then
+    the combine launch). 16 experts, top-4: tokens share experts, so plan
+    entries carry several slots."""
     host, pool = pool16
     d = _pool_desc(16)
     R, X = gen.moe_inputs(16, batch=batch, seed=40 + batch)
