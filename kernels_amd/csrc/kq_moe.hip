@@ -974,7 +974,8 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
         if constexpr (FROM_PLAN) return wgt[sl];
         else return s_wgt[sl];
     };
-    const uint32_t nexp = FROM_PLAN ? plan_g->n : ps.n, npairs = HID >> 1;
+    // (n is at most kMaxSlots by construction; the clamp keeps every plan read in bounds)
+    const uint32_t nexp = min(FROM_PLAN ? plan_g->n : ps.n, (uint32_t)kMaxSlots), npairs = HID >> 1;
     const uint32_t p0 = blockIdx.x * pp, np = p0 < npairs ? min(pp, npairs - p0) : 0;
     const uint32_t N = nexp * np;
     const uint32_t nit = N > wave ? (N - wave + kStWaves - 1) / kStWaves : 0;
