@@ -73,17 +73,30 @@ struct WsLayout {
     size_t lg, cnt, plan, ys, total;
 };
 
-// Workspace: [logits f32 batch x n_experts][completion counter][plan]
-// [per-slot down products f32 batch x top_k x hidden]
+// Workspace: [completion counter][plan][logits f32 batch x n_experts]
+// [per-slot down products f32 batch x top_k x hidden]. The counter and the
+// plan sit at fixed offsets, the same for every batch and descriptor: a
+// workspace sized for a large batch and reused at a smaller one (or the
+// reverse) never has its counter or plan overwritten by another call's
+// logits or products. Every call writes the logits and products it reads.
+constexpr size_t kWsCnt = 0, kWsPlan = 256;
 WsLayout ws_layout(const kq_moe_desc& d, uint32_t batch) {
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
     WsLayout L;
-    L.lg = 0;
-    L.cnt = al(4ull * batch * d.n_experts);
-    L.plan = L.cnt + 256;
-    L.ys = al(L.plan + sizeof(Plan));
+    L.cnt = kWsCnt;
+    L.plan = kWsPlan;
+    L.lg = al(L.plan + sizeof(Plan));
+    L.ys = L.lg + al(4ull * batch * d.n_experts);
     L.total = L.ys + al(4ull * batch * d.top_k * d.hidden);
     return L;
+}
+
+// Valid slot bits of a plan mask word h for nslots slots: a plan read from
+// the workspace is masked with these, so no slot index it yields reaches
+// past the call's nslots slots (wgt, H, ys and the LDS blocks).
+__device__ __forceinline__ uint64_t slot_bits(uint32_t nslots, int h) {
+    const uint32_t n = h ? (nslots > 64 ? nslots - 64 : 0) : (nslots < 64 ? nslots : 64);
+    return n >= 64 ? ~0ull : ((1ull << n) - 1ull);
 }
 
 // Eight consecutive elements as loaded (fp16: one u32x4; fp32: two f32x4).
@@ -410,12 +423,12 @@ __device__ void get_plan(const Plan* plan_g, const uint32_t* idx, const float* w
         if (wgt) s_wgt[tid] = wgt[tid];
     }
     if constexpr (FROM_PLAN) {
-        const uint32_t n = plan_g->n;
+        const uint32_t n = min(plan_g->n, nslots);
         if (tid == 0) ps.n = n;
         for (uint32_t u = tid; u < n; u += blockDim.x) {
             ps.expert[u] = plan_g->expert[u];
-            ps.mask[u][0] = plan_g->mask[u][0];
-            ps.mask[u][1] = plan_g->mask[u][1];
+            ps.mask[u][0] = plan_g->mask[u][0] & slot_bits(nslots, 0);
+            ps.mask[u][1] = plan_g->mask[u][1] & slot_bits(nslots, 1);
         }
         __syncthreads();
     } else {
@@ -502,10 +515,10 @@ __global__ __launch_bounds__(kGuThreads) void moe_gate_up_k(
     uint32_t e, n;
     uint64_t sm0, sm1;
     if constexpr (FROM_PLAN) {
-        n = plan_g->n;
+        n = min(plan_g->n, batch * TK);
         e = plan_g->expert[min(u, (uint32_t)kMaxSlots - 1)];
-        sm0 = plan_g->mask[u][0];
-        sm1 = plan_g->mask[u][1];
+        sm0 = plan_g->mask[min(u, (uint32_t)kMaxSlots - 1)][0] & slot_bits(batch * TK, 0);
+        sm1 = plan_g->mask[min(u, (uint32_t)kMaxSlots - 1)][1] & slot_bits(batch * TK, 1);
     } else {
         __shared__ Plan ps;
         __shared__ uint32_t s_idx[kMaxSlots];
@@ -967,15 +980,16 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
         else return ps.expert[u];
     };
     auto p_mask = [&](uint32_t u, int h) __attribute__((always_inline)) {
-        if constexpr (FROM_PLAN) return plan_g->mask[u][h];
+        if constexpr (FROM_PLAN) return plan_g->mask[u][h] & slot_bits(nslots, h);
         else return ps.mask[u][h];
     };
     auto p_wgt = [&](uint32_t sl) __attribute__((always_inline)) {
         if constexpr (FROM_PLAN) return wgt[sl];
         else return s_wgt[sl];
     };
-    // (n is at most kMaxSlots by construction; the clamp keeps every plan read in bounds)
-    const uint32_t nexp = min(FROM_PLAN ? plan_g->n : ps.n, (uint32_t)kMaxSlots), npairs = HID >> 1;
+    // at most one plan entry per slot; with the masks above, every plan read
+    // and every slot index stays within this call's nslots slots
+    const uint32_t nexp = min(FROM_PLAN ? plan_g->n : ps.n, nslots), npairs = HID >> 1;
     const uint32_t p0 = blockIdx.x * pp, np = p0 < npairs ? min(pp, npairs - p0) : 0;
     const uint32_t N = nexp * np;
     const uint32_t nit = N > wave ? (N - wave + kStWaves - 1) / kStWaves : 0;
@@ -1080,7 +1094,8 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
     const uint32_t u = blockIdx.y;
     if (u >= plan_g->n) return;  // uniform: fewer distinct experts than slots
     const uint32_t ex = min(plan_g->expert[u], d.n_experts - 1);
-    const uint64_t mk0 = plan_g->mask[u][0], mk1 = plan_g->mask[u][1];
+    const uint64_t mk0 = plan_g->mask[u][0] & slot_bits(batch * TK, 0);
+    const uint64_t mk1 = plan_g->mask[u][1] & slot_bits(batch * TK, 1);
     const uint32_t nvec = __popcll(mk0) + __popcll(mk1);
     const uint32_t i0 = blockIdx.x * rp, ni = i0 < IN ? min(rp, IN - i0) : 0;
     const uint32_t nit = ni > wave ? (ni - wave + kStWaves - 1) / kStWaves : 0;
@@ -1208,7 +1223,8 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_part_k(
     const uint32_t u = blockIdx.y;
     if (u >= plan_g->n) return;  // uniform: fewer distinct experts than slots
     const uint32_t ex = min(plan_g->expert[u], d.n_experts - 1);
-    const uint64_t mk0 = plan_g->mask[u][0], mk1 = plan_g->mask[u][1];
+    const uint64_t mk0 = plan_g->mask[u][0] & slot_bits(nslots, 0);
+    const uint64_t mk1 = plan_g->mask[u][1] & slot_bits(nslots, 1);
     const uint32_t nvec = __popcll(mk0) + __popcll(mk1);
     const uint32_t npairs = HID >> 1, p0 = blockIdx.x * pp;
     const uint32_t np = p0 < npairs ? min(pp, npairs - p0) : 0;

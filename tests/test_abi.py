@@ -100,6 +100,25 @@ def test_moe_desc_and_workspace():
     assert kq.lib().kq_moe_workspace_size(C.byref(d), 17) == 0
 
 
+def test_moe_workspace_head_is_batch_independent():
+    """The workspace is [counter + plan head][logits][per-slot products]: the
+    batch-dependent parts are exactly the logits and the products, so the
+    head (the router's completion counter and the plan, which must survive
+    between calls) sits at the same offsets for every batch and descriptor,
+    and a workspace sized for one batch can serve another."""
+    def al(v):
+        return (v + 255) // 256 * 256
+
+    heads = set()
+    for ne, tk in ((128, 4), (16, 3), (256, 8)):
+        d = kq.moe_default_desc()
+        d.n_experts, d.top_k = ne, tk
+        for b in range(1, 17):
+            n = kq.moe_workspace_size(d, b)
+            heads.add(n - al(4 * b * ne) - al(4 * b * tk * d.hidden))
+    assert len(heads) == 1, heads
+
+
 def test_moe_rejects_on_host():
     L = kq.lib()
     d = kq.moe_default_desc()

@@ -221,6 +221,30 @@ def test_block_expert_partitioned_down(gpu, pool16, batch):
         assert inf_rel(got, Yref) < 2e-3
 
 
+def test_workspace_reused_across_batches(gpu, pool16):
+    """One workspace sized for 16 tokens serves calls at 8, 3, 16 and 1 tokens
+    in turn (every block form: streaming, expert-partitioned gate/up and
+    down, the combine launch): the router's counter and the plan sit at fixed
+    offsets, so no call's logits or products overwrite them."""
+    host, pool = pool16
+    d = _pool_desc(16)
+    wsb = kq.moe_workspace_size(d, 16)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
+    kq.moe_workspace_init(ws, wsb)
+    for batch in (8, 3, 16, 1, 8):
+        R, X = gen.moe_inputs(16, batch=batch, seed=500 + batch)
+        oidx, owgt, lg = oracle.moe_router(R, oracle.F16, X, oracle.F16, batch, odesc(d))
+        assert routing_margin(lg, 4) > 1e-5
+        _, _, Yref = oracle.moe_block(host, odesc(d), R, oracle.F16, X, oracle.F16, batch)
+        b = Block(gpu, d, batch)
+        kq.moe_block(pool, d, dev(R, gpu).view(torch.float16), dev(X, gpu).view(torch.float16),
+                     b.idx, b.wgt, b.H, b.y, ws, wsb, batch=batch)
+        torch.cuda.synchronize()
+        assert np.array_equal(b.idx.cpu().numpy().astype(np.uint32), oidx), f"batch {batch}"
+        assert np.allclose(b.wgt.cpu().numpy(), owgt, atol=1e-6)
+        assert_close(to_f64(b.y), Yref, what=f"shared workspace, batch {batch}")
+
+
 def test_block_fp32_inputs_and_fp16_out(gpu, pool16):
     """Reference-fidelity inputs: fp32 router and x (xh written by the router)."""
     host, pool = pool16
@@ -303,7 +327,7 @@ def _compact_desc(hidden, inter, n_experts, top_k):
 
 
 @pytest.mark.parametrize("hidden,inter,batch", [(1024, 2048, 1), (4096, 512, 2), (2048, 4096, 1),
-                                                (1536, 1024, 3)])
+                                                (1536, 1024, 3), (2048, 2048, 4), (2048, 4096, 3)])
 def test_other_shapes(gpu, hidden, inter, batch):
     """Descriptors other than gpt-oss's (every chunk count of the streaming
     kernels, partial chunks, 16 experts, top-3): the block and the
