@@ -76,17 +76,29 @@ def build_drivers(verbose: bool = False):
         return list(ex.map(lambda n: _driver(n, verbose), DRIVERS))
 
 
-def build(verbose: bool = False, jobs: int = 0) -> str:
+def _fresh(src):
+    """True if src's object is newer than src and every header it may include."""
+    obj = os.path.join(OBJ, os.path.basename(src) + ".o")
+    if not os.path.exists(obj):
+        return False
+    deps = [src] + [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    deps.append(os.path.join(ROOT, "include", "kq.h"))
+    return all(os.path.getmtime(obj) > os.path.getmtime(d) for d in deps)
+
+
+def build(verbose: bool = False, jobs: int = 0, incremental: bool = False) -> str:
+    """Compile every source (incremental=True: only those whose object is
+    older than the source or a header) and link libkq.so and the drivers."""
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
     srcs = sources()
-    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)))
-    objs = []
+    todo = [s for s in srcs if not (incremental and _fresh(s))]
+    jobs = jobs or min(max(1, len(todo)), max(1, (os.cpu_count() or 4)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        for obj, warn in ex.map(lambda s: _compile(s, verbose), srcs):
-            objs.append(obj)
+        for _, warn in ex.map(lambda s: _compile(s, verbose), todo):
             if warn and verbose:
                 print(warn, flush=True)
+    objs = [os.path.join(OBJ, os.path.basename(s) + ".o") for s in srcs]
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs
     if verbose:
@@ -98,4 +110,4 @@ def build(verbose: bool = False, jobs: int = 0) -> str:
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, incremental="-i" in sys.argv))

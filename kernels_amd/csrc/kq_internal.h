@@ -67,10 +67,9 @@ hipError_t launch_moe_gate_up(const uint8_t* pool, const kq_moe_desc& d, const u
 hipError_t launch_moe_down(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
                            const float* wgt, const uint16_t* H, void* Y, bool y_f32,
                            uint32_t batch, hipStream_t s);
-// router logits -> gate/up with in-kernel top-k (publishes idx, wgt) -> down
-// Router logits only (float [batch][n_experts] at ws + 0; xh = half(X) if X is fp32).
+// Router logits only (float [batch][n_experts] to lg; xh = half(X) if X is fp32).
 hipError_t launch_moe_logits(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
-                             const kq_moe_desc& d, uint16_t* xh, void* ws, hipStream_t s);
+                             const kq_moe_desc& d, uint16_t* xh, float* lg, hipStream_t s);
 // One operation per launch, batch 1 (see kq_moe_unfused.hip).
 size_t moe_unfused_ws_bytes(const kq_moe_desc& d);
 uint32_t moe_unfused_launches(const kq_moe_desc& d);

@@ -1351,14 +1351,22 @@ __global__ void fill_zero_k(uint32_t* p, size_t n) {
 
 uint32_t chunks_j(uint32_t K) { return ((K >> 5) + 31) / 32; }
 
+// Router outputs: the logits, and (with the tail) the completion counter and
+// the plan; cnt and plan are unused without the tail.
+struct RtOut {
+    float* lg;
+    uint32_t* cnt;
+    Plan* plan;
+};
+
 template <int IT, bool TAIL>
 hipError_t launch_router_it(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
-                            const kq_moe_desc& d, uint16_t* xh, const WsLayout& L, uint8_t* ws,
-                            uint32_t* idx, float* wgt, hipStream_t s) {
+                            const kq_moe_desc& d, uint16_t* xh, RtOut o, uint32_t* idx,
+                            float* wgt, hipStream_t s) {
     const dim3 grid((d.n_experts + 3) / 4, (batch + 1) / 2);
-    float* lg = reinterpret_cast<float*>(ws + L.lg);
-    uint32_t* cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
-    Plan* plan = reinterpret_cast<Plan*>(ws + L.plan);
+    float* lg = o.lg;
+    uint32_t* cnt = o.cnt;
+    Plan* plan = o.plan;
 #define KQ_RT(RF, XF)                                                                     \
     moe_router_k<RF, XF, IT, TAIL><<<grid, kRtThreads, 0, s>>>(R, X, batch, d.n_experts, d.hidden, \
                                                          d.top_k, xh, lg, cnt, idx, wgt, plan)
@@ -1371,16 +1379,25 @@ hipError_t launch_router_it(const void* R, bool r_f32, const void* X, bool x_f32
 }
 
 template <bool TAIL>
+hipError_t launch_router_o(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
+                           const kq_moe_desc& d, uint16_t* xh, RtOut o, uint32_t* idx, float* wgt,
+                           hipStream_t s) {
+    const uint32_t it = (d.hidden + 511) / 512;  // hidden <= 4096 (validated)
+    if (it <= 2) return launch_router_it<2, TAIL>(R, r_f32, X, x_f32, batch, d, xh, o, idx, wgt, s);
+    if (it <= 4) return launch_router_it<4, TAIL>(R, r_f32, X, x_f32, batch, d, xh, o, idx, wgt, s);
+    if (it <= 6) return launch_router_it<6, TAIL>(R, r_f32, X, x_f32, batch, d, xh, o, idx, wgt, s);
+    return launch_router_it<8, TAIL>(R, r_f32, X, x_f32, batch, d, xh, o, idx, wgt, s);
+}
+
+template <bool TAIL>
 hipError_t launch_router_t(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
                            const kq_moe_desc& d, uint16_t* xh, void* ws, uint32_t* idx, float* wgt,
                            hipStream_t s) {
     const WsLayout L = ws_layout(d, batch);
     uint8_t* w = reinterpret_cast<uint8_t*>(ws);
-    const uint32_t it = (d.hidden + 511) / 512;  // hidden <= 4096 (validated)
-    if (it <= 2) return launch_router_it<2, TAIL>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
-    if (it <= 4) return launch_router_it<4, TAIL>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
-    if (it <= 6) return launch_router_it<6, TAIL>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
-    return launch_router_it<8, TAIL>(R, r_f32, X, x_f32, batch, d, xh, L, w, idx, wgt, s);
+    const RtOut o{reinterpret_cast<float*>(w + L.lg), reinterpret_cast<uint32_t*>(w + L.cnt),
+                  reinterpret_cast<Plan*>(w + L.plan)};
+    return launch_router_o<TAIL>(R, r_f32, X, x_f32, batch, d, xh, o, idx, wgt, s);
 }
 
 // Router with its tail: logits, then (last workgroup) top-k, idx/wgt and plan.
@@ -1597,8 +1614,9 @@ hipError_t launch_dn(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* 
 }  // namespace
 
 hipError_t launch_moe_logits(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
-                             const kq_moe_desc& d, uint16_t* xh, void* ws, hipStream_t s) {
-    return launch_router_t<false>(R, r_f32, X, x_f32, batch, d, xh, ws, nullptr, nullptr, s);
+                             const kq_moe_desc& d, uint16_t* xh, float* lg, hipStream_t s) {
+    return launch_router_o<false>(R, r_f32, X, x_f32, batch, d, xh, RtOut{lg, nullptr, nullptr},
+                                  nullptr, nullptr, s);
 }
 
 size_t moe_ws_bytes(const kq_moe_desc& d, uint32_t batch) { return ws_layout(d, batch).total; }

@@ -37,7 +37,7 @@ struct UWs {
 UWs uws_layout(const kq_moe_desc& d) {
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
     UWs L;
-    L.lg = 0;  // the router writes its logits at workspace offset 0
+    L.lg = 0;
     L.sel = al(4ull * d.n_experts);
     L.g = L.sel + al(4ull * kUMaxTopK);
     L.u = L.g + al(4ull * d.inter);
@@ -157,7 +157,7 @@ hipError_t launch_moe_unfused(const uint8_t* pool, const kq_moe_desc& d, const v
     const Int4Cfg auto_cfg{0, 0};
     hipError_t e;
 
-    if ((e = launch_moe_logits(R, r_f32, X, x_f32, 1, d, xh, ws, s)) != hipSuccess) return e;
+    if ((e = launch_moe_logits(R, r_f32, X, x_f32, 1, d, xh, lg, s)) != hipSuccess) return e;
     u_topk_k<<<1, 64, 0, s>>>(lg, d.n_experts, d.top_k, idx, sel);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     u_softmax_k<<<1, 64, 0, s>>>(sel, d.top_k, wgt);
