@@ -243,6 +243,24 @@ kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d,
                        void* Y, kq_dtype y_dtype, void* ws, size_t ws_bytes,
                        kq_stream_t stream);
 
+/* kq_moe_block without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). It has no counterpart in the reference.
+ * The workspace is a fixed array of KQ_MOE_NOALLOC_WS_BYTES in libkq's own
+ * device memory, one per GPU, held until the process ends; the call
+ * allocates nothing. A (desc, batch) whose kq_moe_workspace_size exceeds
+ * KQ_MOE_NOALLOC_WS_BYTES returns KQ_EWORKSPACE (gpt-oss-120b shapes fit up
+ * to 16 tokens). The first call on a GPU looks the array up and zero-fills
+ * it with a kernel on `stream`. Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (different streams, or different
+ * host threads, without ordering between them) race and must not be made.
+ * Otherwise the same arguments, results and launches as kq_moe_block. */
+#define KQ_MOE_NOALLOC_WS_BYTES (1u << 20)
+kq_status kq_moe_block_noalloc(const uint8_t* pool, const kq_moe_desc* d,
+                               const void* R, kq_dtype r_dtype, const void* X, kq_dtype x_dtype,
+                               uint32_t batch, uint32_t* idx, float* wgt, uint16_t* xh,
+                               uint16_t* H, void* Y, kq_dtype y_dtype, kq_stream_t stream);
+
 /* The same block with one operation per launch, one token: router logits,
  * top-k, softmax, then per slot gate GEMV, up GEMV, SwiGLU, and per slot
  * down GEMV, weighted accumulate -- 3 + 5 * top_k launches (23 at top-4),

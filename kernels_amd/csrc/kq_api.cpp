@@ -281,10 +281,11 @@ kq_status kq_moe_down_combine(const uint8_t* pool, const kq_moe_desc* d, const u
                                           reinterpret_cast<hipStream_t>(stream)));
 }
 
-kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d, const void* R, kq_dtype r_dtype,
-                       const void* X, kq_dtype x_dtype, uint32_t batch, uint32_t* idx, float* wgt,
-                       uint16_t* xh, uint16_t* H, void* Y, kq_dtype y_dtype, void* ws,
-                       size_t ws_bytes, kq_stream_t stream) {
+namespace {
+// Arguments of the block (everything but the workspace).
+kq_status check_block(const uint8_t* pool, const kq_moe_desc* d, const void* R, kq_dtype r_dtype,
+                      const void* X, kq_dtype x_dtype, uint32_t batch, uint32_t* idx, float* wgt,
+                      uint16_t* xh, uint16_t* H, void* Y, kq_dtype y_dtype) {
     kq_status st = check_desc(d, batch);
     if (st != KQ_OK) return st;
     if (!pool || !R || !X || !idx || !wgt || !H || !Y) return KQ_ENULL;
@@ -298,10 +299,33 @@ kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d, const void* R,
         return KQ_EALIGN;
     if (xh && !aligned(xh, 16)) return KQ_EALIGN;
     if (!aligned(Y, y_dtype == KQ_F32 ? 4 : 2)) return KQ_EALIGN;
+    return KQ_OK;
+}
+}  // namespace
+
+kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d, const void* R, kq_dtype r_dtype,
+                       const void* X, kq_dtype x_dtype, uint32_t batch, uint32_t* idx, float* wgt,
+                       uint16_t* xh, uint16_t* H, void* Y, kq_dtype y_dtype, void* ws,
+                       size_t ws_bytes, kq_stream_t stream) {
+    kq_status st = check_block(pool, d, R, r_dtype, X, x_dtype, batch, idx, wgt, xh, H, Y, y_dtype);
+    if (st != KQ_OK) return st;
     if ((st = check_ws(d, batch, ws, ws_bytes)) != KQ_OK) return st;
     return hip_status(kq::launch_moe_block(pool, *d, R, r_dtype == KQ_F32, X, x_dtype == KQ_F32,
                                            batch, idx, wgt, xh, H, Y, y_dtype == KQ_F32, ws,
                                            reinterpret_cast<hipStream_t>(stream)));
+}
+
+kq_status kq_moe_block_noalloc(const uint8_t* pool, const kq_moe_desc* d, const void* R,
+                               kq_dtype r_dtype, const void* X, kq_dtype x_dtype, uint32_t batch,
+                               uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H, void* Y,
+                               kq_dtype y_dtype, kq_stream_t stream) {
+    kq_status st = check_block(pool, d, R, r_dtype, X, x_dtype, batch, idx, wgt, xh, H, Y, y_dtype);
+    if (st != KQ_OK) return st;
+    if (kq::moe_ws_bytes(*d, batch) > KQ_MOE_NOALLOC_WS_BYTES) return KQ_EWORKSPACE;
+    return hip_status(kq::launch_moe_block_noalloc(pool, *d, R, r_dtype == KQ_F32, X,
+                                                   x_dtype == KQ_F32, batch, idx, wgt, xh, H, Y,
+                                                   y_dtype == KQ_F32,
+                                                   reinterpret_cast<hipStream_t>(stream)));
 }
 
 size_t kq_moe_unfused_workspace_size(const kq_moe_desc* d) {

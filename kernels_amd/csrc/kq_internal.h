@@ -76,6 +76,11 @@ uint32_t moe_unfused_launches(const kq_moe_desc& d);
 hipError_t launch_moe_unfused(const uint8_t* pool, const kq_moe_desc& d, const void* R, bool r_f32,
                               const void* X, bool x_f32, uint32_t* idx, float* wgt, uint16_t* xh,
                               uint16_t* H, void* Y, bool y_f32, void* ws, hipStream_t s);
+// kq_moe_block on the per-device static workspace (no allocation).
+hipError_t launch_moe_block_noalloc(const uint8_t* pool, const kq_moe_desc& d, const void* R,
+                                    bool r_f32, const void* X, bool x_f32, uint32_t batch,
+                                    uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H, void* Y,
+                                    bool y_f32, hipStream_t s);
 hipError_t launch_moe_block(const uint8_t* pool, const kq_moe_desc& d, const void* R, bool r_f32,
                             const void* X, bool x_f32, uint32_t batch, uint32_t* idx, float* wgt,
                             uint16_t* xh, uint16_t* H, void* Y, bool y_f32, void* ws,

@@ -44,11 +44,19 @@
 // Activations are used as permuted fp16 pairs with per-chunk sums (the
 // AND-OR dequant of kq_device.h); bf16 group scale and bias apply once per
 // 32-weight chunk.
+#include <mutex>
+
 #include "kq_device.h"
 #include "kq_internal.h"
 #include "kq_moe_device.h"
 
 namespace kq {
+
+// Workspace of kq_moe_block_noalloc: one array per GPU in the code object's
+// own device memory, held until the process ends. Host code never passes
+// `scratch` itself to a kernel (on the host the name is only a stand-in for
+// the symbol); it uses the per-device address hipGetSymbolAddress returns.
+static __device__ __align__(256) uint8_t scratch[KQ_MOE_NOALLOC_WS_BYTES];
 
 namespace {
 
@@ -1611,7 +1619,42 @@ hipError_t launch_dn(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* 
     return hipGetLastError();
 }
 
+// Per-device address of `scratch`, looked up once per device (with that
+// device current) at the first kq_moe_block_noalloc call on it. The zero
+// fill at set-up is a kernel on the caller's stream (graph-safe), ahead of
+// the first block that uses the array.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+hipError_t scratch_ptr(void** out, hipStream_t s) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch[dev] == nullptr) {
+        void* p = nullptr;
+        if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+        if (p == nullptr) return hipErrorInvalidSymbol;
+        if ((e = launch_ws_zero(p, KQ_MOE_NOALLOC_WS_BYTES, s)) != hipSuccess) return e;
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return hipSuccess;
+}
+
 }  // namespace
+
+hipError_t launch_moe_block_noalloc(const uint8_t* pool, const kq_moe_desc& d, const void* R,
+                                    bool r_f32, const void* X, bool x_f32, uint32_t batch,
+                                    uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H, void* Y,
+                                    bool y_f32, hipStream_t s) {
+    void* ws = nullptr;
+    const hipError_t e = scratch_ptr(&ws, s);
+    if (e != hipSuccess) return e;
+    return launch_moe_block(pool, d, R, r_f32, X, x_f32, batch, idx, wgt, xh, H, Y, y_f32, ws, s);
+}
 
 hipError_t launch_moe_logits(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
                              const kq_moe_desc& d, uint16_t* xh, float* lg, hipStream_t s) {

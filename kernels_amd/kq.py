@@ -24,7 +24,8 @@ EXPORTS = ("kq_status_str", "kq_last_hip_error", "kq_version", "kq_int4_gemv",
            "kq_int4_gemv_path", "kq_int4_gemv_cfg", "kq_xsum32", "kq_stream_read",
            "kq_vq_gemv", "kq_moe_default_desc", "kq_moe_workspace_size",
            "kq_moe_workspace_init", "kq_moe_router_topk", "kq_moe_gate_up_swiglu",
-           "kq_moe_down_combine", "kq_moe_block", "kq_moe_unfused_workspace_size",
+           "kq_moe_down_combine", "kq_moe_block", "kq_moe_block_noalloc",
+           "kq_moe_unfused_workspace_size",
            "kq_moe_block_unfused", "kq_vq_quantize_workspace_size", "kq_vq_quantize")
 
 
@@ -83,6 +84,8 @@ def lib():
                                           sz, vp]
         L.kq_moe_block.argtypes = [vp, C.POINTER(MoEDesc), vp, i32, vp, i32, u32, vp, vp, vp, vp,
                                    vp, i32, vp, sz, vp]
+        L.kq_moe_block_noalloc.argtypes = [vp, C.POINTER(MoEDesc), vp, i32, vp, i32, u32, vp, vp,
+                                           vp, vp, vp, i32, vp]
         L.kq_moe_unfused_workspace_size.argtypes = [C.POINTER(MoEDesc)]
         L.kq_moe_unfused_workspace_size.restype = sz
         L.kq_moe_block_unfused.argtypes = [vp, C.POINTER(MoEDesc), vp, i32, vp, i32, u32, vp, vp,
@@ -269,6 +272,18 @@ def moe_block(pool, desc, R, x, idx, wgt, H, y, ws, ws_bytes, batch=1, xh=None, 
     _check(lib().kq_moe_block(_ptr(pool), C.byref(desc), _ptr(R), _dt(R), _ptr(x), _dt(x), batch,
                               _ptr(idx), _ptr(wgt), _ptr(xh), _ptr(H), _ptr(y), _dt(y), _ptr(ws),
                               ws_bytes, _stream(stream)), "kq_moe_block")
+
+
+MOE_NOALLOC_WS_BYTES = 1 << 20  # KQ_MOE_NOALLOC_WS_BYTES
+
+
+def moe_block_noalloc(pool, desc, R, x, idx, wgt, H, y, batch=1, xh=None, stream=None):
+    """moe_block on libkq's per-GPU static workspace: no allocation, no
+    workspace argument (no reference counterpart; for callers that cannot
+    allocate). Calls that overlap on one GPU race."""
+    _check(lib().kq_moe_block_noalloc(_ptr(pool), C.byref(desc), _ptr(R), _dt(R), _ptr(x), _dt(x),
+                                      batch, _ptr(idx), _ptr(wgt), _ptr(xh), _ptr(H), _ptr(y),
+                                      _dt(y), _stream(stream)), "kq_moe_block_noalloc")
 
 
 def moe_unfused_workspace_size(desc):

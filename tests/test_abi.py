@@ -119,6 +119,30 @@ def test_moe_workspace_head_is_batch_independent():
     assert len(heads) == 1, heads
 
 
+def test_moe_noalloc_rejects_on_host():
+    """kq_moe_block_noalloc refuses, before any launch, a (desc, batch) whose
+    workspace exceeds its static array, and validates like kq_moe_block."""
+    L = kq.lib()
+    d = kq.moe_default_desc()
+    assert kq.moe_workspace_size(d, 16) <= kq.MOE_NOALLOC_WS_BYTES  # gpt-oss fits at 16 tokens
+    big = kq.moe_default_desc()
+    big.hidden, big.inter, big.top_k = 4096, 4096, 8
+    big.off_up = big.off_down = big.sub_s = big.sub_b = big.sub_bi = 0
+    big.blob = 4096 * 4096
+    assert kq.moe_workspace_size(big, 16) > kq.MOE_NOALLOC_WS_BYTES
+
+    def call(desc, batch, **kw):
+        a = dict(pool=FAKE, R=FAKE, X=FAKE, idx=FAKE, wgt=FAKE, xh=None, H=FAKE, Y=FAKE)
+        a.update(kw)
+        return L.kq_moe_block_noalloc(a["pool"], C.byref(desc), a["R"], kq.F16, a["X"], kq.F16,
+                                      batch, a["idx"], a["wgt"], a["xh"], a["H"], a["Y"], kq.F32,
+                                      None)
+    assert call(big, 16) == kq.KQ_EWORKSPACE
+    assert call(d, 17) == kq.KQ_EINVAL
+    assert call(d, 1, pool=None) == kq.KQ_ENULL
+    assert call(d, 1, H=FAKE + 2) == kq.KQ_EALIGN
+
+
 def test_moe_rejects_on_host():
     L = kq.lib()
     d = kq.moe_default_desc()
