@@ -24,10 +24,12 @@
 //     (wave64 DPP reduction, store); with P > 1 (short matrices, to fill the
 //     CUs) the P partial sums of a round meet in LDS in a fixed order;
 //   * each wave streams its (row group, step) items through a ring of D
-//     register slots; every load is unconditional (rows and padding steps are
-//     clamped to valid addresses, results discarded) and first used by the
-//     compute of its own item, and the prologue's issue order is pinned, so
-//     the waitcnt pass waits for exactly one slot at a time.
+//     register slots, as deep as its items when registers allow (all of a
+//     wave's loads then issue before its first compute); every load is
+//     unconditional (rows are clamped to valid addresses, results discarded;
+//     padding slots load out of range: zeros, no traffic) and first used by
+//     the compute of its own item, and the prologue's issue order is pinned,
+//     so the waitcnt pass waits for exactly one slot at a time.
 #include "kq_device.h"
 #include "kq_internal.h"
 
@@ -97,8 +99,10 @@ __host__ __device__ inline size_t vlds_x(uint32_t ntok, uint32_t nchp) {
 constexpr uint32_t kXBlk = 4608;
 constexpr int kXr = 8;  // x words a thread stages per pass (one pass up to 8 x threads)
 
+// Register budget: a ring of R * D >= 16 row-steps needs more than 128
+// VGPRs, so those instantiations run at most 8 waves per workgroup.
 template <int NB, int R, int D, bool SB, bool BF, bool GA>
-__global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
+__global__ __launch_bounds__(R * D >= 16 ? 512 : 1024) void int4_valu(VArgs A) {
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr uint32_t MB = SB ? 4 : 2;  // metadata bytes per group and array
     constexpr uint32_t kOOB = 0x80000000u;  // past every descriptor's range: loads read zeros
@@ -177,14 +181,19 @@ __global__ __launch_bounds__(1024) void int4_valu(VArgs A) {
     const uint32_t vm_full = (lane >> A.cshift) * MB, vm_last = cl < nch ? vm_full : kOOB;
     VSlot<R, SB> ring[D];
     auto issue = [&](VSlot<R, SB>& e, Cursor c) __attribute__((always_inline)) {
-        if (c.round >= A.rounds) {  // padding item: re-read the last real one
+        // padding item (the ring depth past the wave's items): every lane
+        // loads out of range, which returns zeros and moves no bytes; the
+        // item's compute is skipped
+        const bool pad = c.round >= A.rounds;  // uniform
+        if (pad) {
             c.round = A.rounds - 1;
             c.j = A.J - 1;
         }
         const uint32_t grp = min(g0 + c.round * A.Q + q, last_group);
         const uint32_t s = __builtin_amdgcn_readfirstlane(p * A.J + c.j);
         const bool last = s == nstep - 1;
-        const uint32_t vw = last ? vw_last : vw_full, vm = last ? vm_last : vm_full;
+        const uint32_t vw = pad ? kOOB : last ? vw_last : vw_full;
+        const uint32_t vm = pad ? kOOB : last ? vm_last : vm_full;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t rr = __builtin_amdgcn_readfirstlane(min(grp * R + r, last_row) - row0);
@@ -343,44 +352,57 @@ uint32_t log2u(uint32_t v) {
 // Launch plan: R rows per item, P K-parts, Q row-group lanes, ring depth D.
 // Measured on MI355X (Llama / 70B shapes, batch 1), the plan (1) spreads the
 // row groups over every CU, (2) keeps the per-CU bytes minimal (no idle
-// lanes: Q is cut to the rows a CU has), and (3) uses D = 2 -- deeper rings
-// measured slower at every shape. Among (R, P) with equal per-CU work, one x
-// read shared by 2 rows and a single K part win (4096 x 14336: P = 1 7.7 us,
-// P = 7 9.1 us).
+// lanes: Q is cut to the rows a CU has), (3) among (R, P) with equal per-CU
+// work, one x read shared by 2 rows and a single K part win (4096 x 14336:
+// P = 1 7.7 us, P = 7 9.1 us), and (4) D = 2: deeper rings, up to all of a
+// wave's items in flight at once, measured slower at every shape
+// (4096 x 14336: D = 2 / 4 / 8 / 16 took 7.6 / 8.1 / 9.6 / 11.2 us;
+// 14336 x 4096: 7.7 / 9.5 / 9.8 / 10.4 us). Deeper rings (forced plans
+// only) cap the workgroup at 8 waves when R * D >= 16.
 bool make_vplan(uint32_t M, uint32_t K, uint32_t ntok, Int4Cfg cfg, VPlan& out) {
     const uint32_t nch = K >> 5, nstep = (nch + 63) / 64, nchp = nstep * 64, cu = cu_count();
-    if (cfg.unroll != 0 && cfg.unroll != 2 && cfg.unroll != 4 && cfg.unroll != 8) return false;
+    if (cfg.unroll != 0 && cfg.unroll != 2 && cfg.unroll != 4 && cfg.unroll != 8 &&
+        cfg.unroll != 16)
+        return false;
     bool found = false;
     double best = 0.0;
     for (uint32_t R = 2; R >= 1; --R) {
         for (uint32_t P = 1; P <= kMaxWaves; ++P) {
             if (nstep % P) continue;
             if (cfg.rows > 0 && (uint32_t)cfg.rows != P) continue;
-            const uint32_t D = cfg.unroll > 0 ? (uint32_t)cfg.unroll : 2;
-            if (R == 2 && D == 8) continue;  // register budget: 2 rows x 8 slots
             const uint32_t ngroups = (M + R - 1) / R, J = nstep / P;
             const uint32_t per_cu = (ngroups + cu - 1) / cu;
-            const uint32_t qmax = kMaxWaves / P;
-            const uint32_t rounds = (per_cu + qmax - 1) / qmax;
-            const uint32_t Q = (per_cu + rounds - 1) / rounds;
-            const uint32_t waves = P * Q, groups_wg = rounds * Q;
-            const uint32_t nwg = (ngroups + groups_wg - 1) / groups_wg;
-            const uint32_t nreal = rounds * J;
-            const uint32_t nsteps = (nreal + D - 1) / D * D;
-            const size_t lds = vlds_x(ntok, nchp) + (P > 1 ? (size_t)rounds * waves * R * ntok * 4 : 0);
-            if (lds > kLdsMax) continue;
-            // per-CU KiB (padding included) plus a latency term for short
-            // waves: fewer than 8 waves or fewer than 2 items leave HBM idle.
-            double cost = (double)nsteps * waves * R;
-            if (waves < 8) cost *= 1.0 + 0.1 * (8 - waves);
-            // K parts: a wave finishes (reduces) its rows once per item
-            // instead of once per row -- measured 4-17% slower per part count
-            if (P > 1) cost *= 1.0 + 0.05 * P;
-            if (R == 2) cost *= 0.98;
-            if (!found || cost < best) {
-                found = true;
-                best = cost;
-                out = VPlan{R, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, lds};
+            // up to 16 waves with a ring of R * D < 16 row-steps, or up to 8
+            // waves with a ring of up to 16 items
+            for (uint32_t wcap = kMaxWaves; wcap >= 8; wcap /= 2) {
+                if (P > wcap) continue;
+                const uint32_t dmax = wcap > 8 ? 8 / R : (ntok == 2 && R == 2 ? 8 : 16);
+                if (cfg.unroll > 0 && (uint32_t)cfg.unroll > dmax) continue;
+                const uint32_t qmax = wcap / P;
+                const uint32_t rounds = (per_cu + qmax - 1) / qmax;
+                const uint32_t Q = (per_cu + rounds - 1) / rounds;
+                const uint32_t waves = P * Q, groups_wg = rounds * Q;
+                const uint32_t nwg = (ngroups + groups_wg - 1) / groups_wg;
+                const uint32_t nreal = rounds * J;
+                const uint32_t D = cfg.unroll > 0 ? (uint32_t)cfg.unroll : 2;
+                if (R * D >= 16 && waves > 8) continue;
+                const uint32_t nsteps = (nreal + D - 1) / D * D;
+                const size_t lds =
+                    vlds_x(ntok, nchp) + (P > 1 ? (size_t)rounds * waves * R * ntok * 4 : 0);
+                if (lds > kLdsMax) continue;
+                // per-CU KiB plus a latency term for short waves: fewer than 8
+                // waves or fewer than 2 items leave HBM idle.
+                double cost = (double)nreal * waves * R;
+                if (waves < 8) cost *= 1.0 + 0.1 * (8 - waves);
+                // K parts: a wave finishes (reduces) its rows once per item
+                // instead of once per row -- measured 4-17% slower per part count
+                if (P > 1) cost *= 1.0 + 0.05 * P;
+                if (R == 2) cost *= 0.98;
+                if (!found || cost < best) {
+                    found = true;
+                    best = cost;
+                    out = VPlan{R, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, lds};
+                }
             }
         }
     }
@@ -405,9 +427,10 @@ hipError_t vgo_d(const VArgs& a, const VPlan& pl, hipStream_t s) {
     switch (pl.D) {
         case 2: return vgo<NB, R, 2, SB, BF, GA>(a, pl, s);
         case 4: return vgo<NB, R, 4, SB, BF, GA>(a, pl, s);
-        case 8:
-            if constexpr (R == 1) return vgo<NB, R, 8, SB, BF, GA>(a, pl, s);
-            else return hipErrorInvalidValue;
+        case 8: return vgo<NB, R, 8, SB, BF, GA>(a, pl, s);
+        case 16:  // two tokens on two rows: a 16-deep ring would spill
+            if constexpr (NB == 2 && R == 2) return hipErrorInvalidValue;
+            else return vgo<NB, R, 16, SB, BF, GA>(a, pl, s);
         default: return hipErrorInvalidValue;
     }
 }

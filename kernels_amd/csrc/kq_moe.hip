@@ -26,11 +26,12 @@
 //      (at one token, held in registers); down keeps per-slot
 //      wgt * (down . h + bias) in LDS and sums the slots in k order;
 //    - expert-partitioned (the block's gate/up from 3 tokens, moe_gu_part_k;
-//      its down from 6 tokens, moe_dn_part_k): workgroup (row chunk, plan
-//      entry) streams one expert's rows with only that expert's
-//      activations in LDS; down writes per-slot products to the workspace
-//      and a small moe_combine_k launch sums them in slot order (4
-//      launches in all);
+//      its down from 6 tokens, moe_dn_part_k): one round of one workgroup
+//      per CU; each plan entry gets workgroups in proportion to its cost
+//      (rows x (4 + 3 x slots)), and a workgroup streams a row chunk of one
+//      expert with only that expert's activations in LDS; down writes
+//      per-slot products to the workspace and a small moe_combine_k launch
+//      sums them in slot order (4 launches in all);
 //    - per tile (moe_gate_up_k, moe_down_k): the standalone entry points
 //      past the streaming limits (they take no workspace): a grid of
 //      (16-row tile, expert) or 8-output-row workgroups that issue all of
@@ -62,7 +63,6 @@ namespace {
 
 constexpr int kMaxSlots = 128;  // batch (16) x top_k (8)
 constexpr int kMaxTopK = 8;
-constexpr int kRtThreads = 256;  // router: 4 experts per workgroup
 constexpr int kGuThreads = 256;  // gate/up: 4 waves
 constexpr int kGuRW = 4;         // gate/up rows per wave
 constexpr int kGuRows = 16;      // gate/up rows per workgroup
@@ -234,14 +234,14 @@ __device__ void build_plan(const uint32_t* s_idx, uint32_t nslots, uint32_t NE, 
 // elements 8(l + 64i), i < IT (IT * 512 >= hidden); every router and x load
 // is issued before the first multiply (addresses clamped, results past the
 // row masked), so a wave pays one memory round trip.
-template <bool RF32, bool XF32, int IT, bool TAIL>
-__global__ __launch_bounds__(kRtThreads) void moe_router_k(
+template <bool RF32, bool XF32, int IT, bool TAIL, int NW>
+__global__ __launch_bounds__(64 * NW) void moe_router_k(
     const void* __restrict__ R, const void* __restrict__ X, uint32_t batch, uint32_t NE,
     uint32_t HID, uint32_t TK, uint16_t* __restrict__ xh, float* lg, uint32_t* cnt,
     uint32_t* __restrict__ idx_out, float* __restrict__ wgt_out, Plan* __restrict__ plan_out) {
     constexpr int NBT = 2;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t e = blockIdx.x * (kRtThreads / 64) + wave, ec = min(e, NE - 1);
+    const uint32_t e = blockIdx.x * (NW) + wave, ec = min(e, NE - 1);
     const uint32_t t0 = blockIdx.y * NBT;
     Raw8<RF32> r[IT];
     Raw8<XF32> x[NBT][IT];
@@ -254,8 +254,8 @@ __global__ __launch_bounds__(kRtThreads) void moe_router_k(
             x[t][i] = load8<XF32>(X, (size_t)min(t0 + t, batch - 1) * HID + k);
     }
     if (XF32 && xh) {  // fp16 copy of x for the projections, spread over the grid
-        const uint32_t tot = batch * HID, nthr = gridDim.x * gridDim.y * kRtThreads;
-        for (uint32_t i = (blockIdx.y * gridDim.x + blockIdx.x) * kRtThreads + tid; i < tot;
+        const uint32_t tot = batch * HID, nthr = gridDim.x * gridDim.y * (64 * NW);
+        for (uint32_t i = (blockIdx.y * gridDim.x + blockIdx.x) * (64 * NW) + tid; i < tot;
              i += nthr)
             xh[i] = f2h(reinterpret_cast<const float*>(X)[i]);
     }
@@ -300,7 +300,7 @@ __global__ __launch_bounds__(kRtThreads) void moe_router_k(
     __shared__ float s_wgt[kMaxSlots];
     __shared__ uint32_t bits[8];
     __shared__ Plan ps;
-    for (uint32_t t = wave; t < batch; t += kRtThreads / 64)
+    for (uint32_t t = wave; t < batch; t += NW)
         topk_wave<true>(lg + (size_t)t * NE, NE, TK, s_idx + t * TK, s_wgt + t * TK);
     __syncthreads();
     const uint32_t nslots = batch * TK;
@@ -312,7 +312,7 @@ __global__ __launch_bounds__(kRtThreads) void moe_router_k(
     if (plan_out) {
         const uint32_t n = ps.n;
         if (tid == 0) plan_out->n = n;
-        for (uint32_t u = tid; u < n; u += kRtThreads) {
+        for (uint32_t u = tid; u < n; u += (64 * NW)) {
             plan_out->expert[u] = ps.expert[u];
             plan_out->mask[u][0] = ps.mask[u][0];
             plan_out->mask[u][1] = ps.mask[u][1];
@@ -1083,29 +1083,112 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
     }
 }
 
-// Gate/up + SwiGLU, partitioned by expert (3-16 tokens; about two workgroups
-// per CU -- at 8 tokens 116.3 us per block against 130.3 with one and 118.4
-// with four; the per-tile kernel gave 119.0): workgroup (c, u)
-// streams rows [c * rp, (c + 1) * rp) of the plan's u-th expert (half 0 the
-// gate row, half 1 the up row) with only the x vectors of that expert's
-// tokens in LDS, and writes h for each of its slots. Each expert's rows are
-// read once for all its slots, as in the other forms.
+// One-round expert partition (the block's gate/up and down from 3 tokens):
+// G workgroups, one per CU; expert u of the plan gets a share of them in
+// proportion to its cost, rows * (kPartRow + kPartSlot * slots of u) -- a
+// row's weight bytes plus one dot product per slot that chose the expert,
+// so experts picked by several tokens get more workgroups (at least one
+// each) -- and splits its nrows rows (gate/up rows or down row pairs)
+// evenly among them. Workgroup b's expert u starts at
+// start(u) = u + floor((G - n) * C_u / W), C_u the cost of the experts
+// before u, W the total. Each wave computes the assignment itself: lane l
+// loads plan entries l and l + 64 with vector loads (one round trip), a
+// wave prefix sum gives every C_u, a ballot finds b's entry, and its expert
+// and slot masks come back by readlane.
+// Costs measured at 8 tokens: a row of a two-slot expert took 1.45x the
+// time of a one-slot row. Ring depth 4 (long per-wave streams here, ~40
+// items): 8 / 16 tokens 99.8 / 179.5 -> 98.8 / 170.9 us per block.
+constexpr uint32_t kPartRow = 4, kPartSlot = 3;
+constexpr int kPartD = 4;
+struct PartAssign {
+    uint32_t u, r0, nr, ex;  // u = 0xFFFFFFFF: no work for this workgroup
+    uint64_t m0, m1;
+};
+__device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
+    const uint32_t lane = threadIdx.x & 63;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t t = __shfl_up(v, d, 64);
+        if (lane >= (uint32_t)d) v += t;
+    }
+    return v;
+}
+__device__ __forceinline__ uint32_t rl(uint32_t v, uint32_t l) {
+    return __builtin_amdgcn_readlane(v, l);
+}
+__device__ __forceinline__ uint64_t rl64(uint64_t v, uint32_t l) {
+    return (uint64_t)rl((uint32_t)v, l) | ((uint64_t)rl((uint32_t)(v >> 32), l) << 32);
+}
+__device__ __forceinline__ PartAssign part_assign(const Plan* plan_g, uint32_t nslots, uint32_t nrows,
+                                                  uint32_t n_experts) {
+    const uint32_t lane = threadIdx.x & 63, G = gridDim.x, b = blockIdx.x;
+    const uint64_t sb0 = slot_bits(nslots, 0), sb1 = slot_bits(nslots, 1);
+    // every entry's loads first (entries past n are read but unused)
+    uint64_t m0[2], m1[2];
+    uint32_t ex[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const uint32_t u = lane + 64 * q;
+        m0[q] = plan_g->mask[u][0] & sb0;
+        m1[q] = plan_g->mask[u][1] & sb1;
+        ex[q] = min(plan_g->expert[u], n_experts - 1);
+    }
+    const uint32_t n = min(plan_g->n, nslots);
+    PartAssign a{0xFFFFFFFFu, 0, 0, 0, 0, 0};
+    if (n == 0 || G < n) return a;
+    uint32_t c[2], sc[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+        c[q] = lane + 64 * q < n ? kPartRow + kPartSlot * (uint32_t)(__popcll(m0[q]) + __popcll(m1[q]))
+                                 : 0u;
+    sc[0] = wave_scan_incl(c[0]);
+    const uint32_t tot0 = rl(sc[0], 63);
+    sc[1] = wave_scan_incl(c[1]) + tot0;
+    const uint32_t W = rl(sc[1], 63), spare = G - n;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const uint32_t u = lane + 64 * q;
+        const uint32_t start = u + spare * (sc[q] - c[q]) / W, next = u + 1 + spare * sc[q] / W;
+        const uint64_t hit = __ballot(u < n && start <= b && b < next);
+        if (hit) {  // uniform
+            const uint32_t l = (uint32_t)__builtin_ctzll(hit);
+            const uint32_t st = rl(start, l), nu = rl(next, l) - st, cb = b - st;
+            a.u = l + 64 * q;
+            a.r0 = cb * nrows / nu;
+            a.nr = (cb + 1) * nrows / nu - a.r0;
+            a.ex = rl(ex[q], l);
+            a.m0 = rl64(m0[q], l);
+            a.m1 = rl64(m1[q], l);
+            return a;
+        }
+    }
+    return a;
+}
+
+// Gate/up + SwiGLU, partitioned by expert (3-16 tokens): workgroup b
+// streams the row chunk part_assign gives it of one plan entry's expert
+// (half 0 the gate row, half 1 the up row) with only the x vectors of that
+// expert's tokens in LDS, and writes h for each of its slots. Each expert's
+// rows are read once for all its slots, as in the other forms. One round of
+// one workgroup per CU with cost-weighted chunks replaced two rounds of
+// equal chunks (two workgroups per CU's worth, which ran as two rounds at
+// this register use): 8 tokens 110.6 -> 98.8 us per block with the down
+// kernel done the same way.
 template <int J>
 __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
     const uint8_t* __restrict__ pool, kq_moe_desc d, const Plan* __restrict__ plan_g,
-    const uint16_t* __restrict__ xh, uint32_t batch, uint16_t* __restrict__ H, uint32_t rp) {
+    const uint16_t* __restrict__ xh, uint32_t batch, uint16_t* __restrict__ H) {
     extern __shared__ __align__(16) unsigned char act[];  // [nvec x blocks]
     const uint32_t K = d.hidden, IN = d.inter, TK = d.top_k, nw = K >> 3, nch = K >> 5;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t half = lane >> 5, rowb = K >> 1, metab = (K >> 6) * 2;
-    const uint32_t u = blockIdx.y;
-    if (u >= plan_g->n) return;  // uniform: fewer distinct experts than slots
-    const uint32_t ex = min(plan_g->expert[u], d.n_experts - 1);
-    const uint64_t mk0 = plan_g->mask[u][0] & slot_bits(batch * TK, 0);
-    const uint64_t mk1 = plan_g->mask[u][1] & slot_bits(batch * TK, 1);
+    const PartAssign pa = part_assign(plan_g, batch * TK, IN, d.n_experts);
+    if (pa.u == 0xFFFFFFFFu) return;  // uniform: no share of the plan
+    const uint32_t ex = pa.ex;
+    const uint64_t mk0 = pa.m0, mk1 = pa.m1;
     const uint32_t nvec = __popcll(mk0) + __popcll(mk1);
-    const uint32_t i0 = blockIdx.x * rp, ni = i0 < IN ? min(rp, IN - i0) : 0;
+    const uint32_t i0 = pa.r0, ni = pa.nr;
     const uint32_t nit = ni > wave ? (ni - wave + kStWaves - 1) / kStWaves : 0;
 
     // 1. x of the expert's tokens, slot order: word tid of vector k (K <= 4096: nw <= threads)
@@ -1125,7 +1208,7 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
     // 2. prime the ring: rows i0 + wave, + kStWaves, ... of one expert
     const StLane<J> L = st_lane<J>(half ? d.off_up : d.off_gate, d, K, 0, 0, 0);
     const rsrc_t r = make_rsrc(pool + (size_t)ex * d.blob, (uint32_t)d.blob);
-    constexpr int D = 2;
+    constexpr int D = kPartD;
     StSlot<J> ring[D];
     uint32_t nis = 0;
     auto issue = [&](StSlot<J>& e) __attribute__((always_inline)) {
@@ -1209,8 +1292,8 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
 }
 
 // Down + weighted products, partitioned by expert (from 6 tokens, where the
-// slots' h vectors no longer fit one workgroup's LDS): workgroup (c, u)
-// streams row pairs [c * pp, (c + 1) * pp) of the plan's u-th expert with
+// slots' h vectors no longer fit one workgroup's LDS): workgroup b streams
+// the row-pair chunk part_assign gives it of one plan entry's expert with
 // only that expert's h vectors in LDS (one per slot that chose it, at most
 // one per token), and writes wgt_s * (down . h_s + bias) for each of those
 // slots s to ys[s][*]. moe_combine_k then sums each token's slots in k
@@ -1222,20 +1305,18 @@ template <int J>
 __global__ __launch_bounds__(64 * kStWaves) void moe_dn_part_k(
     const uint8_t* __restrict__ pool, kq_moe_desc d, const float* __restrict__ wgt,
     const Plan* __restrict__ plan_g, const uint16_t* __restrict__ H, uint32_t nslots,
-    float* __restrict__ ys, uint32_t pp) {
+    float* __restrict__ ys) {
     extern __shared__ __align__(16) unsigned char act[];  // [nvec h blocks]
     const uint32_t HID = d.hidden, K = d.inter, nw = K >> 3, nch = K >> 5;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t half = lane >> 5, rowb = K >> 1, metab = (K >> 6) * 2;
-    const uint32_t u = blockIdx.y;
-    if (u >= plan_g->n) return;  // uniform: fewer distinct experts than slots
-    const uint32_t ex = min(plan_g->expert[u], d.n_experts - 1);
-    const uint64_t mk0 = plan_g->mask[u][0] & slot_bits(nslots, 0);
-    const uint64_t mk1 = plan_g->mask[u][1] & slot_bits(nslots, 1);
+    const PartAssign pa = part_assign(plan_g, nslots, HID >> 1, d.n_experts);
+    if (pa.u == 0xFFFFFFFFu) return;  // uniform: no share of the plan
+    const uint32_t ex = pa.ex;
+    const uint64_t mk0 = pa.m0, mk1 = pa.m1;
     const uint32_t nvec = __popcll(mk0) + __popcll(mk1);
-    const uint32_t npairs = HID >> 1, p0 = blockIdx.x * pp;
-    const uint32_t np = p0 < npairs ? min(pp, npairs - p0) : 0;
+    const uint32_t p0 = pa.r0, np = pa.nr;
     const uint32_t nit = np > wave ? (np - wave + kStWaves - 1) / kStWaves : 0;
 
     // 1. the expert's h vectors, slot order: word tid of vector k (K <= 4096: nw <= threads)
@@ -1255,7 +1336,7 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_part_k(
     // 2. prime the ring: row pairs p0 + wave, + kStWaves, ... of one expert
     const StLane<J> L = st_lane<J>(d.off_down, d, K, half * rowb, half * metab, half * 2);
     const rsrc_t r = make_rsrc(pool + (size_t)ex * d.blob, (uint32_t)d.blob);
-    constexpr int D = 2;
+    constexpr int D = kPartD;
     StSlot<J> ring[D];
     uint32_t nis = 0;
     auto issue = [&](StSlot<J>& e) __attribute__((always_inline)) {
@@ -1371,12 +1452,16 @@ template <int IT, bool TAIL>
 hipError_t launch_router_it(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
                             const kq_moe_desc& d, uint16_t* xh, RtOut o, uint32_t* idx,
                             float* wgt, hipStream_t s) {
-    const dim3 grid((d.n_experts + 3) / 4, (batch + 1) / 2);
+    // with the tail: 4 waves (experts) per workgroup, so the last workgroup
+    // has 4 waves for the per-token top-k; logits only: one wave per
+    // workgroup, spreading the router's read over n_experts CUs
+    constexpr int NW = TAIL ? 4 : 1;
+    const dim3 grid((d.n_experts + NW - 1) / NW, (batch + 1) / 2);
     float* lg = o.lg;
     uint32_t* cnt = o.cnt;
     Plan* plan = o.plan;
 #define KQ_RT(RF, XF)                                                                     \
-    moe_router_k<RF, XF, IT, TAIL><<<grid, kRtThreads, 0, s>>>(R, X, batch, d.n_experts, d.hidden, \
+    moe_router_k<RF, XF, IT, TAIL, NW><<<grid, 64 * NW, 0, s>>>(R, X, batch, d.n_experts, d.hidden, \
                                                          d.top_k, xh, lg, cnt, idx, wgt, plan)
     if (r_f32 && x_f32) KQ_RT(true, true);
     else if (r_f32) KQ_RT(true, false);
@@ -1499,19 +1584,22 @@ hipError_t launch_gu_st(const uint8_t* pool, const kq_moe_desc& d, const uint32_
     }
 }
 
+// One round: one workgroup per CU (the partitioned kernels run one 8-wave
+// workgroup per CU at their register use), and at least one per plan entry.
+uint32_t part_grid(const kq_moe_desc& d, uint32_t batch) {
+    const uint32_t nslots = batch * d.top_k;
+    const uint32_t nu = nslots < d.n_experts ? nslots : d.n_experts;  // plan entries at most
+    return cu_count() > nu ? cu_count() : nu;
+}
+
 template <int J>
 hipError_t go_gu_part(const uint8_t* pool, const kq_moe_desc& d, const Plan* plan,
                       const uint16_t* xh, uint16_t* H, uint32_t batch, hipStream_t s) {
     auto kern = moe_gu_part_k<J>;
-    const uint32_t nslots = batch * d.top_k;
-    const uint32_t nu = nslots < d.n_experts ? nslots : d.n_experts;  // plan entries at most
-    const uint32_t nchunk = 2 * cu_count() / nu > 0 ? 2 * cu_count() / nu : 1;
-    const uint32_t rp = (d.inter + nchunk - 1) / nchunk;
     const size_t lds = st_act_bytes(batch, d.hidden);  // at most one slot per token per expert
     const hipError_t e = st_lds(kern, lds);
     if (e != hipSuccess) return e;
-    kern<<<dim3((d.inter + rp - 1) / rp, nu), 64 * kStWaves, lds, s>>>(pool, d, plan, xh, batch, H,
-                                                                        rp);
+    kern<<<part_grid(d, batch), 64 * kStWaves, lds, s>>>(pool, d, plan, xh, batch, H);
     return hipGetLastError();
 }
 
@@ -1548,22 +1636,17 @@ hipError_t launch_gu(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* 
     }
 }
 
-// Row chunks: about two workgroups per CU over the plan's experts (measured
-// at 8 tokens: 119.4 us per block against 123.1 with one and 122.6 with four).
+// One round of cost-weighted row chunks (part_assign), then the combine.
 template <int J>
 hipError_t go_dn_part(const uint8_t* pool, const kq_moe_desc& d, const float* wgt,
                       const Plan* plan, const uint16_t* H, void* Y, bool y_f32, uint32_t batch,
                       float* ys, hipStream_t s) {
     auto kern = moe_dn_part_k<J>;
-    const uint32_t nslots = batch * d.top_k, npairs = d.hidden / 2;
-    const uint32_t nu = nslots < d.n_experts ? nslots : d.n_experts;  // plan entries at most
-    const uint32_t nchunk = 2 * cu_count() / nu > 0 ? 2 * cu_count() / nu : 1;
-    const uint32_t pp = (npairs + nchunk - 1) / nchunk;
+    const uint32_t nslots = batch * d.top_k;
     const size_t lds = st_act_bytes(batch, d.inter);  // at most one slot per token per expert
     hipError_t e = st_lds(kern, lds);
     if (e != hipSuccess) return e;
-    kern<<<dim3((npairs + pp - 1) / pp, nu), 64 * kStWaves, lds, s>>>(pool, d, wgt, plan, H,
-                                                                       nslots, ys, pp);
+    kern<<<part_grid(d, batch), 64 * kStWaves, lds, s>>>(pool, d, wgt, plan, H, nslots, ys);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const uint32_t n = batch * d.hidden;
     moe_combine_k<<<(n + 255) / 256, 256, 0, s>>>(ys, Y, y_f32 ? 1 : 0, batch, d.top_k, d.hidden);

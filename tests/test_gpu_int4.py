@@ -106,8 +106,8 @@ def test_batched_valu(gpu, batch):
 # (K parts, ring depth) per K: parts divide the 1 KiB steps of a row
 # (8192: 4 steps; 2880: 2 steps, the last one partial; 28672: 14 steps)
 VALU_PLANS = [(8192, 1, 2), (8192, 1, 8), (8192, 2, 4), (8192, 4, 2), (8192, 4, 8),
-              (2880, 1, 4), (2880, 2, 2), (2880, 2, 8),
-              (28672, 1, 8), (28672, 2, 4), (28672, 7, 2), (28672, 14, 8)]
+              (8192, 1, 16), (2880, 1, 4), (2880, 2, 2), (2880, 2, 8), (2880, 1, 16),
+              (28672, 1, 8), (28672, 2, 4), (28672, 7, 2), (28672, 14, 8), (28672, 1, 16)]
 
 
 @pytest.mark.parametrize("K,parts,depth", VALU_PLANS)
@@ -121,7 +121,8 @@ def test_forced_launch_shapes_agree(gpu, K, parts, depth, M, batch):
     check(got, ref_int4(p), f"P={parts} D={depth} K={K} M={M} b={batch}")
 
 
-@pytest.mark.parametrize("parts,depth,batch", [(2, 2, 1), (2, 4, 2), (4, 2, 1)])
+@pytest.mark.parametrize("parts,depth,batch", [(2, 2, 1), (2, 4, 2), (4, 2, 1), (1, 16, 1),
+                                               (2, 16, 1), (1, 8, 2)])
 def test_forced_kparts_many_rounds(gpu, parts, depth, batch):
     """K parts over several rounds of row groups per workgroup: every
     round's partial sums wait in LDS until the one reduction at the end."""
