@@ -46,6 +46,7 @@
 // AND-OR dequant of kq_device.h); bf16 group scale and bias apply once per
 // 32-weight chunk.
 #include <mutex>
+#include <type_traits>
 
 #include "kq_device.h"
 #include "kq_internal.h"
@@ -199,28 +200,25 @@ __device__ __forceinline__ void topk_wave(const float* L, uint32_t NE, uint32_t 
 // Plan of the slots s_idx[0 .. nslots) into ps (all threads of the workgroup).
 __device__ void build_plan(const uint32_t* s_idx, uint32_t nslots, uint32_t NE, Plan& ps,
                            uint32_t* bits) {
+    // O(1) per thread: mark the selected experts, rank each slot's expert by
+    // the marks below it, OR the slot into its entry's mask
     const uint32_t tid = threadIdx.x;
     if (tid < 8) bits[tid] = 0;
+    for (uint32_t i = tid; i < 2 * kMaxSlots; i += blockDim.x) ps.mask[i >> 1][i & 1] = 0;
     __syncthreads();
+    uint32_t e = 0;
     if (tid < nslots) {
-        const uint32_t e = min(s_idx[tid], NE - 1);
+        e = min(s_idx[tid], NE - 1);
         atomicOr(&bits[e >> 5], 1u << (e & 31));
     }
     __syncthreads();
-    for (uint32_t e = tid; e < NE; e += blockDim.x) {
+    if (tid < nslots) {
         const uint32_t w = e >> 5, b = e & 31;
-        if (!((bits[w] >> b) & 1u)) continue;
         uint32_t rank = __popc(bits[w] & ((1u << b) - 1u));
         for (uint32_t i = 0; i < w; ++i) rank += __popc(bits[i]);
-        uint64_t m0 = 0, m1 = 0;
-        for (uint32_t s = 0; s < nslots; ++s)
-            if (min(s_idx[s], NE - 1) == e) {
-                if (s < 64) m0 |= 1ull << s;
-                else m1 |= 1ull << (s - 64);
-            }
-        ps.expert[rank] = e;
-        ps.mask[rank][0] = m0;
-        ps.mask[rank][1] = m1;
+        ps.expert[rank] = e;  // every slot of the expert writes the same value
+        atomicOr(reinterpret_cast<unsigned long long*>(&ps.mask[rank][tid >> 6]),
+                 1ull << (tid & 63));
     }
     if (tid == 0) {
         uint32_t n = 0;
@@ -840,6 +838,23 @@ __device__ __forceinline__ float st_dotx(const StDq<J>& q, const StX<J>& x) {
     return acc;
 }
 
+// st_dotx with the dequantisation folded in chunk by chunk (one activation
+// vector: the dequantised words are not reused, so they need not all be live).
+template <int J>
+__device__ __forceinline__ float st_dotx_dq(const StSlot<J>& e, const DequantConsts& kc,
+                                            const StX<J>& x) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const u32x4 d0 = dq4(e.w[j].x, kc), d1 = dq4(e.w[j].y, kc);
+        const u32x4 d2 = dq4(e.w[j].z, kc), d3 = dq4(e.w[j].w, kc);
+        const float da = dot4(d2, x.p[j][2], dot4(d0, x.p[j][0], 0.0f));
+        const float db = dot4(d3, x.p[j][3], dot4(d1, x.p[j][1], 0.0f));
+        acc = fmaf(bf2f(e.s[j]), (da + db) - x.k[j].y, fmaf(bf2f(e.b[j]), x.k[j].x, acc));
+    }
+    return acc;
+}
+
 // Gate/up: items are (distinct expert u, row i) in u-major order; workgroup
 // w takes a contiguous range, wave q every kStWaves-th item of it. Half 0
 // reads gate row i, half 1 up row i. XREG (one token): the token's
@@ -1174,16 +1189,39 @@ __device__ __forceinline__ PartAssign part_assign(const Plan* plan_g, uint32_t n
 // equal chunks (two workgroups per CU's worth, which ran as two rounds at
 // this register use): 8 tokens 110.6 -> 98.8 us per block with the down
 // kernel done the same way.
+// The routing comes from the router's logits lg ([batch][n_experts], a
+// logits-only router launch before this one): every workgroup runs the
+// top-k of every token (wave w takes tokens w, w + 8) and builds the plan in
+// LDS; workgroup 0 publishes idx, wgt and the plan for the down launch.
+// Every token's x is loaded at entry, ahead of the logits, and staged in LDS
+// by token, so the staging never waits behind the weight ring.
 template <int J>
 __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
-    const uint8_t* __restrict__ pool, kq_moe_desc d, const Plan* __restrict__ plan_g,
-    const uint16_t* __restrict__ xh, uint32_t batch, uint16_t* __restrict__ H) {
-    extern __shared__ __align__(16) unsigned char act[];  // [nvec x blocks]
-    const uint32_t K = d.hidden, IN = d.inter, TK = d.top_k, nw = K >> 3, nch = K >> 5;
-    const uint32_t tid = threadIdx.x, lane = tid & 63;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint8_t* __restrict__ pool, kq_moe_desc d, const uint16_t* __restrict__ xh,
+    uint32_t batch, uint16_t* __restrict__ H, const float* __restrict__ lg,
+    uint32_t* __restrict__ idx_out, float* __restrict__ wgt_out, Plan* __restrict__ plan_out) {
+    extern __shared__ __align__(16) unsigned char act[];  // [batch x blocks], by token
+    __shared__ Plan ps;
+    __shared__ uint32_t s_idx[kMaxSlots];
+    __shared__ float s_wgt[kMaxSlots];
+    __shared__ uint32_t bits[8];
+    const uint32_t K = d.hidden, IN = d.inter, TK = d.top_k;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t half = lane >> 5, rowb = K >> 1, metab = (K >> 6) * 2;
-    const PartAssign pa = part_assign(plan_g, batch * TK, IN, d.n_experts);
+
+    // 1. every token's x (K <= 4096, batch <= 16: at most kStXr words per thread)
+    StStage st;
+    st_stage_load(st, xh, batch, K);
+    // 2. top-k of every token, then the plan
+    for (uint32_t t = wave; t < batch; t += kStWaves)
+        topk_wave<false>(lg + (size_t)t * d.n_experts, d.n_experts, TK, s_idx + t * TK,
+                         s_wgt + t * TK);
+    __syncthreads();
+    build_plan(s_idx, batch * TK, d.n_experts, ps, bits);
+    if (blockIdx.x == 0) publish_plan(ps, s_idx, s_wgt, batch * TK, idx_out, wgt_out, plan_out);
+    // 3. this workgroup's expert and rows (the same in every wave)
+    const PartAssign pa = part_assign(&ps, batch * TK, IN, d.n_experts);
     if (pa.u == 0xFFFFFFFFu) return;  // uniform: no share of the plan
     const uint32_t ex = pa.ex;
     const uint64_t mk0 = pa.m0, mk1 = pa.m1;
@@ -1191,21 +1229,7 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
     const uint32_t i0 = pa.r0, ni = pa.nr;
     const uint32_t nit = ni > wave ? (ni - wave + kStWaves - 1) / kStWaves : 0;
 
-    // 1. x of the expert's tokens, slot order: word tid of vector k (K <= 4096: nw <= threads)
-    const rsrc_t rx = make_rsrc(xh, batch * K * 2);
-    u32x4 sv[kStXr];
-    {
-        uint64_t a = mk0, b = mk1;
-#pragma unroll
-        for (int k = 0; k < kStXr; ++k) {
-            if ((uint32_t)k < nvec) {  // uniform
-                const uint32_t tok = pop_slot(a, b) / TK;
-                sv[k] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rx, tid < nw ? tid * 16 : kStOOB, __builtin_amdgcn_readfirstlane(tok * K * 2), 0);
-            }
-        }
-    }
-    // 2. prime the ring: rows i0 + wave, + kStWaves, ... of one expert
+    // 4. prime the ring: rows i0 + wave, + kStWaves, ... of one expert
     const StLane<J> L = st_lane<J>(half ? d.off_up : d.off_gate, d, K, 0, 0, 0);
     const rsrc_t r = make_rsrc(pool + (size_t)ex * d.blob, (uint32_t)d.blob);
     constexpr int D = kPartD;
@@ -1218,37 +1242,13 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
         st_issue<J>(e, r, L, i * rowb, i * metab, i * 2);
         ++nis;
     };
-    // primed on every path (same load count: the staging waits only for its own loads)
 #pragma unroll
     for (int q = 0; q < D; ++q) {
         issue(ring[q]);
         __builtin_amdgcn_sched_barrier(0);
     }
-    // 3. staging store: permuted pairs and chunk constants, chunks past K zero
-#pragma unroll
-    for (int k = 0; k < kStXr; ++k) {
-        if ((uint32_t)k < nvec) {  // uniform
-            float cs, cc;
-            word_consts(sv[k], cs, cc);
-            cs = quad_sum(cs);
-            cc = quad_sum(cc);
-            if (tid < nw) {
-                const uint32_t ch = tid >> 2, jw = tid & 3;
-                unsigned char* blk = act + (k * J + (ch >> 5)) * kABlk;
-                *reinterpret_cast<u32x4*>(blk + jw * 512 + (ch & 31) * 16) = pair_perm(sv[k]);
-                if (jw == 0)
-                    *reinterpret_cast<float2*>(blk + 2048 + (ch & 31) * 8) = make_float2(cs, cc);
-            }
-        }
-    }
-    const uint32_t npad = 32 * J - nch;
-    for (uint32_t i = tid; i < nvec * 5 * npad; i += blockDim.x) {
-        const uint32_t v = i / (5 * npad), rem = i - v * 5 * npad, jw = rem / npad;
-        const uint32_t ch = nch + (rem - jw * npad);
-        unsigned char* blk = act + (v * J + (ch >> 5)) * kABlk;
-        if (jw < 4) *reinterpret_cast<u32x4*>(blk + jw * 512 + (ch & 31) * 16) = u32x4{0, 0, 0, 0};
-        else *reinterpret_cast<float2*>(blk + 2048 + (ch & 31) * 8) = make_float2(0.0f, 0.0f);
-    }
+    // 5. staging store (vector = token), chunks past K zero
+    st_stage_store<J>(st, act, batch, K);
     __syncthreads();
     if (nit == 0) return;  // no later barrier
 
@@ -1256,39 +1256,54 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
     const DequantConsts kc;
     // One store per step by every lane (lane j < nvec: slot j; the rest repeat
     // the last), so the next ring wait does not also wait for it; only the
-    // tail checks for padding.
-    auto step = [&](const StSlot<J>& e, uint32_t it, bool tail) __attribute__((always_inline)) {
-        if (tail && it >= nit) return;  // padding (uniform)
-        const uint32_t i = i0 + wave + it * kStWaves;
-        StDq<J> q;
-        st_dequant<J>(e, kc, q);
-        const float bg = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 0));
-        const float bu = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 32));
-        uint64_t a = mk0, b = mk1;
-        size_t oi = 0;
-        uint16_t ov = 0;
-        for (uint32_t k = 0; k < nvec; ++k) {
-            const uint32_t sl = pop_slot(a, b);
-            const float2 hs = half_sums(st_dot<J>(q, act, k));
-            const uint16_t hv = f2h(swiglu(hs.x + bg, hs.y + bu));
-            if (lane >= k) {
-                oi = (size_t)sl * IN + i;
-                ov = hv;
+    // tail checks for padding. XR (one slot, the common case): the token's x
+    // chunks are held in registers, so the loop reads no LDS.
+    auto run = [&](auto xr_tag) __attribute__((always_inline)) {
+        constexpr bool XR = decltype(xr_tag)::value;
+        StX<J> xr;
+        if constexpr (XR) {
+            uint64_t ma = mk0, mb = mk1;
+            st_xload<J>(xr, act, pop_slot(ma, mb) / TK);
+        }
+        auto step = [&](const StSlot<J>& e, uint32_t it, bool tail) __attribute__((always_inline)) {
+            if (tail && it >= nit) return;  // padding (uniform)
+            const uint32_t i = i0 + wave + it * kStWaves;
+            StDq<J> q;
+            if constexpr (!XR) st_dequant<J>(e, kc, q);
+            const float bg = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 0));
+            const float bu = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 32));
+            uint64_t ma = mk0, mb = mk1;
+            size_t oi = 0;
+            uint16_t ov = 0;
+            for (uint32_t k = 0; k < (XR ? 1u : nvec); ++k) {
+                const uint32_t sl = pop_slot(ma, mb);
+                float acc;
+                if constexpr (XR) acc = st_dotx_dq<J>(e, kc, xr);
+                else acc = st_dot<J>(q, act, sl / TK);
+                const float2 hs = half_sums(acc);
+                const uint16_t hv = f2h(swiglu(hs.x + bg, hs.y + bu));
+                if (lane >= k) {
+                    oi = (size_t)sl * IN + i;
+                    ov = hv;
+                }
+            }
+            H[oi] = ov;
+        };
+        const uint32_t nsteps = (nit + D - 1) / D * D;
+        uint32_t it = 0;
+        for (; it + D < nsteps; it += D) {
+#pragma unroll
+            for (int q = 0; q < D; ++q) {
+                step(ring[q], it + q, false);
+                issue(ring[q]);
             }
         }
-        H[oi] = ov;
+#pragma unroll
+        for (int q = 0; q < D; ++q) step(ring[q], it + q, true);
     };
-    const uint32_t nsteps = (nit + D - 1) / D * D;
-    uint32_t it = 0;
-    for (; it + D < nsteps; it += D) {
-#pragma unroll
-        for (int q = 0; q < D; ++q) {
-            step(ring[q], it + q, false);
-            issue(ring[q]);
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < D; ++q) step(ring[q], it + q, true);
+    // (at J = 4 the registers of the one-slot form would spill)
+    if (J <= 3 && nvec == 1) run(std::integral_constant<bool, J <= 3>{});  // uniform
+    else run(std::false_type{});
 }
 
 // Down + weighted products, partitioned by expert (from 6 tokens, where the
@@ -1593,21 +1608,33 @@ uint32_t part_grid(const kq_moe_desc& d, uint32_t batch) {
 }
 
 template <int J>
-hipError_t go_gu_part(const uint8_t* pool, const kq_moe_desc& d, const Plan* plan,
-                      const uint16_t* xh, uint16_t* H, uint32_t batch, hipStream_t s) {
+hipError_t go_gu_part(const uint8_t* pool, const kq_moe_desc& d, const uint16_t* xh, uint16_t* H,
+                      uint32_t batch, GuTopk tk, hipStream_t s) {
     auto kern = moe_gu_part_k<J>;
-    const size_t lds = st_act_bytes(batch, d.hidden);  // at most one slot per token per expert
+    const size_t lds = st_act_bytes(batch, d.hidden);  // every token's x
     const hipError_t e = st_lds(kern, lds);
     if (e != hipSuccess) return e;
-    kern<<<part_grid(d, batch), 64 * kStWaves, lds, s>>>(pool, d, plan, xh, batch, H);
+    kern<<<part_grid(d, batch), 64 * kStWaves, lds, s>>>(pool, d, xh, batch, H, tk.lg, tk.idx,
+                                                          tk.wgt, tk.plan);
     return hipGetLastError();
 }
 
-// The expert-partitioned gate/up: up to kStXr tokens, hidden <= one word per
-// thread, the x blocks in LDS.
+hipError_t launch_gu_part(const uint8_t* pool, const kq_moe_desc& d, const uint16_t* xh,
+                          uint16_t* H, uint32_t batch, GuTopk tk, hipStream_t s) {
+    switch (chunks_j(d.hidden)) {
+        case 1: return go_gu_part<1>(pool, d, xh, H, batch, tk, s);
+        case 2: return go_gu_part<2>(pool, d, xh, H, batch, tk, s);
+        case 3: return go_gu_part<3>(pool, d, xh, H, batch, tk, s);
+        case 4: return go_gu_part<4>(pool, d, xh, H, batch, tk, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// The expert-partitioned gate/up: every token's x staged in one pass (at
+// most kStXr words per thread) and in LDS next to the plan.
 bool gu_part_ok(const kq_moe_desc& d, uint32_t batch) {
     return batch <= (uint32_t)kStXr && (d.hidden >> 3) <= 64u * kStWaves &&
-           d.blob < (1ull << 31) && st_act_bytes(batch, d.hidden) + 1024 <= kLdsMax;
+           d.blob < (1ull << 31) && st_act_bytes(batch, d.hidden) + kStStatic <= kLdsMax;
 }
 
 template <bool FP>
@@ -1616,17 +1643,6 @@ hipError_t launch_gu(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* 
                      hipStream_t s) {
     if (gu_streams(d, batch))
         return launch_gu_st<FP ? 1 : 0>(pool, d, idx, plan, xh, H, batch, GuTopk{}, s);
-    if constexpr (FP) {  // the plan is in the workspace
-        if (gu_part_ok(d, batch)) {
-            switch (chunks_j(d.hidden)) {
-                case 1: return go_gu_part<1>(pool, d, plan, xh, H, batch, s);
-                case 2: return go_gu_part<2>(pool, d, plan, xh, H, batch, s);
-                case 3: return go_gu_part<3>(pool, d, plan, xh, H, batch, s);
-                case 4: return go_gu_part<4>(pool, d, plan, xh, H, batch, s);
-                default: return hipErrorInvalidValue;
-            }
-        }
-    }
     switch (chunks_j(d.hidden)) {
         case 1: return go_gu<1, FP>(pool, d, idx, plan, xh, H, batch, s);
         case 2: return go_gu<2, FP>(pool, d, idx, plan, xh, H, batch, s);
@@ -1792,6 +1808,14 @@ hipError_t launch_moe_block(const uint8_t* pool, const kq_moe_desc& d, const voi
         if (e != hipSuccess) return e;
         const GuTopk tk{reinterpret_cast<const float*>(w + L.lg), idx, wgt, plan};
         e = launch_gu_st<2>(pool, d, idx, plan, xin, H, batch, tk, s);
+    } else if (gu_part_ok(d, batch)) {
+        // logits only; every partitioned gate/up workgroup runs the top-k
+        // and builds the plan, workgroup 0 publishes it (measured at 8
+        // tokens: the router with its device-wide top-k tail took 11.5 us)
+        e = launch_router_t<false>(R, r_f32, X, x_f32, batch, d, xh, ws, idx, wgt, s);
+        if (e != hipSuccess) return e;
+        const GuTopk tk{reinterpret_cast<const float*>(w + L.lg), idx, wgt, plan};
+        e = launch_gu_part(pool, d, xin, H, batch, tk, s);
     } else {
         e = launch_router(R, r_f32, X, x_f32, batch, d, xh, ws, idx, wgt, s);
         if (e != hipSuccess) return e;
