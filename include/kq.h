@@ -109,6 +109,16 @@ kq_status kq_xsum32(const uint16_t* X, float* xs, uint32_t K, uint32_t batch,
  * Replaces: stream_read int4-gemv/src/kernels.metal:260-283. */
 kq_status kq_stream_read(const void* src, size_t bytes, uint32_t* sink, kq_stream_t stream);
 
+/* kq_stream_read with the launch shape of the reference's ceiling sweep:
+ * `unroll` (1, 2, 4 or 8) independent loads in flight per thread, over
+ * `threads` threads (a multiple of 256). kq_stream_read uses the best
+ * shape measured on MI355X (unroll 1, 2048 x 256 threads).
+ * Replaces: stream_read with function constant UNROLL and its dispatch
+ * size int4-gemv/src/kernels.metal:260-283, swept by
+ * int4-gemv/src/main.mm:294-334. */
+kq_status kq_stream_read_cfg(const void* src, size_t bytes, uint32_t* sink, uint32_t unroll,
+                             uint32_t threads, kq_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Codebook (VQ, d = 2, 256 entries) dequant-GEMV
  *

@@ -187,7 +187,19 @@ kq_status kq_stream_read(const void* src, size_t bytes, uint32_t* sink, kq_strea
     if (!src || !sink) return KQ_ENULL;
     if (bytes == 0 || bytes % 16) return KQ_EINVAL;
     if (!aligned(src, 16)) return KQ_EALIGN;
-    return hip_status(kq::launch_stream_read(src, bytes, sink, reinterpret_cast<hipStream_t>(stream)));
+    return hip_status(
+        kq::launch_stream_read(src, bytes, sink, 0, 0, reinterpret_cast<hipStream_t>(stream)));
+}
+
+kq_status kq_stream_read_cfg(const void* src, size_t bytes, uint32_t* sink, uint32_t unroll,
+                             uint32_t threads, kq_stream_t stream) {
+    if (!src || !sink) return KQ_ENULL;
+    if (bytes == 0 || bytes % 16) return KQ_EINVAL;
+    if (!(unroll == 1 || unroll == 2 || unroll == 4 || unroll == 8)) return KQ_EINVAL;
+    if (threads == 0 || threads % 256 || threads > (1u << 30)) return KQ_EINVAL;
+    if (!aligned(src, 16)) return KQ_EALIGN;
+    return hip_status(kq::launch_stream_read(src, bytes, sink, unroll, threads,
+                                             reinterpret_cast<hipStream_t>(stream)));
 }
 
 kq_status kq_vq_gemv(const uint8_t* IDX, const uint16_t* C, const uint16_t* S, const uint16_t* X,

@@ -535,9 +535,13 @@ hipError_t launch_xsum32(const uint16_t* X, float* xs, uint32_t K, uint32_t batc
 }
 
 // ---------------------------------------------------------------------------
-// Streaming-read ceiling (int4-gemv/src/kernels.metal:260-283): U independent
-// 16-byte non-temporal loads per thread in flight, XOR-folded so the loads
-// cannot be eliminated; the sink is written only if the fold is all ones.
+// Streaming-read ceiling (int4-gemv/src/kernels.metal:260-283): a grid-stride
+// read, U independent 16-byte non-temporal loads per thread in flight,
+// XOR-folded so the loads cannot be eliminated; the sink is written only if
+// the fold is all ones. The reference's harness sweeps U and the thread
+// count and keeps the best (int4-gemv/src/main.mm:294-334); so does
+// bench.py. Default shape: U = 1 over 2048 x 256 threads, the best of that
+// sweep on MI355X (1 GiB: 7.0 TB/s against 5.9 for U = 4 over 8192 x 256).
 // ---------------------------------------------------------------------------
 template <int U>
 __global__ __launch_bounds__(256) void stream_read_k(const u32x4* __restrict__ src, size_t nq,
@@ -563,13 +567,19 @@ __global__ __launch_bounds__(256) void stream_read_k(const u32x4* __restrict__ s
     if (r == 0xFFFFFFFFu) sink[0] = r;
 }
 
-hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t s) {
-    constexpr int U = 4;
+hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, uint32_t unroll,
+                              uint32_t threads, hipStream_t s) {
     const size_t nq = bytes / 16;
-    size_t blocks = (nq + 256 * U - 1) / (256 * U);
-    if (blocks > 8192) blocks = 8192;
-    if (blocks == 0) blocks = 1;
-    stream_read_k<U><<<(unsigned)blocks, 256, 0, s>>>(reinterpret_cast<const u32x4*>(src), nq, sink);
+    if (unroll == 0) unroll = 1;
+    const unsigned blocks = threads ? threads / 256 : 2048;
+    const u32x4* p = reinterpret_cast<const u32x4*>(src);
+    switch (unroll) {
+        case 1: stream_read_k<1><<<blocks, 256, 0, s>>>(p, nq, sink); break;
+        case 2: stream_read_k<2><<<blocks, 256, 0, s>>>(p, nq, sink); break;
+        case 4: stream_read_k<4><<<blocks, 256, 0, s>>>(p, nq, sink); break;
+        case 8: stream_read_k<8><<<blocks, 256, 0, s>>>(p, nq, sink); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -40,7 +40,9 @@ Int4Cfg int4_mfma_default(uint32_t M, uint32_t K, uint32_t batch);
 uint32_t int4_mfma_tokens_per_pass(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg);
 
 hipError_t launch_xsum32(const uint16_t* X, float* xs, uint32_t K, uint32_t batch, hipStream_t s);
-hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t s);
+// unroll 0 and threads 0: the default shape (U = 1, 2048 x 256 threads)
+hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, uint32_t unroll,
+                              uint32_t threads, hipStream_t s);
 
 bool vq_supported(uint32_t M, uint32_t K, uint32_t rows_per_cb);
 hipError_t launch_vq(const uint8_t* IDX, const uint16_t* C, const uint16_t* S, const uint16_t* X,

@@ -22,6 +22,7 @@ PATH_AUTO, PATH_VALU, PATH_MFMA = 0, 1, 2
 # every symbol include/kq.h declares
 EXPORTS = ("kq_status_str", "kq_last_hip_error", "kq_version", "kq_int4_gemv",
            "kq_int4_gemv_path", "kq_int4_gemv_cfg", "kq_xsum32", "kq_stream_read",
+           "kq_stream_read_cfg",
            "kq_vq_gemv", "kq_moe_default_desc", "kq_moe_workspace_size",
            "kq_moe_workspace_init", "kq_moe_router_topk", "kq_moe_gate_up_swiglu",
            "kq_moe_down_combine", "kq_moe_block", "kq_moe_block_noalloc",
@@ -71,6 +72,7 @@ def lib():
                                        i32, i32, vp]
         L.kq_xsum32.argtypes = [vp, vp, u32, u32, vp]
         L.kq_stream_read.argtypes = [vp, sz, vp, vp]
+        L.kq_stream_read_cfg.argtypes = [vp, sz, vp, u32, u32, vp]
         L.kq_vq_gemv.argtypes = [vp, vp, vp, vp, vp, i32, u32, u32, u32, u32, u32, vp]
         L.kq_moe_default_desc.argtypes = [C.POINTER(MoEDesc)]
         L.kq_moe_default_desc.restype = None
@@ -182,8 +184,15 @@ def xsum32(x, xs, K, batch=1, stream=None):
     _check(lib().kq_xsum32(_ptr(x), _ptr(xs), K, batch, _stream(stream)), "kq_xsum32")
 
 
-def stream_read(src, nbytes, sink, stream=None):
-    _check(lib().kq_stream_read(_ptr(src), nbytes, _ptr(sink), _stream(stream)), "kq_stream_read")
+def stream_read(src, nbytes, sink, stream=None, unroll=0, threads=0):
+    """Streaming-read ceiling; unroll/threads > 0 set the launch shape of the
+    reference's sweep (int4-gemv/src/main.mm:294-334)."""
+    if unroll or threads:
+        _check(lib().kq_stream_read_cfg(_ptr(src), nbytes, _ptr(sink), unroll, threads,
+                                        _stream(stream)), "kq_stream_read_cfg")
+    else:
+        _check(lib().kq_stream_read(_ptr(src), nbytes, _ptr(sink), _stream(stream)),
+               "kq_stream_read")
 
 
 # ---------------------------------------------------------------------------

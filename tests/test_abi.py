@@ -219,3 +219,8 @@ def test_stream_read_and_xsum_reject_on_host():
     assert L.kq_stream_read(FAKE, 100, FAKE, None) == kq.KQ_EINVAL
     assert L.kq_stream_read(None, 1024, FAKE, None) == kq.KQ_ENULL
     assert L.kq_xsum32(FAKE, FAKE, 100, 1, None) == kq.KQ_EINVAL
+    assert L.kq_stream_read_cfg(FAKE, 1024, FAKE, 3, 256, None) == kq.KQ_EINVAL  # unroll
+    assert L.kq_stream_read_cfg(FAKE, 1024, FAKE, 4, 300, None) == kq.KQ_EINVAL  # threads % 256
+    assert L.kq_stream_read_cfg(FAKE, 1024, FAKE, 4, 0, None) == kq.KQ_EINVAL
+    assert L.kq_stream_read_cfg(FAKE + 4, 1024, FAKE, 4, 256, None) == kq.KQ_EALIGN
+    assert L.kq_stream_read_cfg(None, 1024, FAKE, 4, 256, None) == kq.KQ_ENULL

@@ -54,26 +54,31 @@ def _sink(gpu):
     return torch.full((1,), SENTINEL, dtype=torch.int32, device=gpu)
 
 
+# (unroll, threads): the default shape, and shapes of the reference's sweep
+SHAPES = [(0, 0), (1, 256), (2, 1024 * 256), (4, 8192 * 256), (8, 2048 * 256)]
+
+
+@pytest.mark.parametrize("unroll,threads", SHAPES)
 @pytest.mark.parametrize("nbytes", [16, 4096, 33_067_008, 16 * 1_000_003])
-def test_stream_read_reads_every_quad(gpu, nbytes):
+def test_stream_read_reads_every_quad(gpu, nbytes, unroll, threads):
     nq = nbytes // 16
     buf = torch.zeros(nq * 4 + 4, dtype=torch.int32, device=gpu)  # one spare quad past the end
     sink = _sink(gpu)
-    kq.stream_read(buf, nbytes, sink)
+    kq.stream_read(buf, nbytes, sink, unroll=unroll, threads=threads)
     torch.cuda.synchronize()
     assert sink.item() == SENTINEL, "all-zero buffer must not set the sink"
     for q in sorted({0, nq // 2, nq - 1, max(0, nq - 257)}):
         buf.zero_()
         buf[4 * q + (q % 4)] = -1  # one word of quad q all ones
         sink = _sink(gpu)
-        kq.stream_read(buf, nbytes, sink)
+        kq.stream_read(buf, nbytes, sink, unroll=unroll, threads=threads)
         torch.cuda.synchronize()
         assert sink.item() == -1, f"quad {q} of {nq} not read"
     # a marker in the quad just past the range is never read
     buf.zero_()
     buf[4 * nq] = -1
     sink = _sink(gpu)
-    kq.stream_read(buf, nbytes, sink)
+    kq.stream_read(buf, nbytes, sink, unroll=unroll, threads=threads)
     torch.cuda.synchronize()
     assert sink.item() == SENTINEL, "read past the range"
 
