@@ -497,18 +497,33 @@ def bench_skinny(torch, kq, dev, args, timer, res):
     res["skinny"] = out
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(seconds):
-    """The reference's CPU int4 GEMV (cpu_gemv_neon, restated for x86 in
-    oracle/cpu_fast.c) over the same Llama layer shapes, on this host's
-    cores, for a bounded sample of about `seconds` of CPU work."""
+    """The reference's CPU int4 GEMV paths (cpu_gemv_neon16 and cpu_gemv_neon,
+    hetero-gemv/src/cpu_gemv.h:55-103, restated for x86 in oracle/cpu_fast.c)
+    over the same Llama layer shapes, on this host's cores, for a bounded
+    sample of about `seconds` of CPU work. Every path the CPU supports is
+    probed on one pass over the layers and the fastest is timed; the rows run
+    on a persistent pool of `cores` threads (all cores of this process's
+    affinity, at most 16: the host share of one GPU on the GPU boxes)."""
     import numpy as np
 
     import oracle
     from kernels_amd import gen
     if not oracle.cpu_fast_supported():
         return None
-    cores = len(os.sched_getaffinity(0))
-    cores = max(1, min(cores, 16))
+    affinity = len(os.sched_getaffinity(0))
+    cores = max(1, min(affinity, 16))
     ncopy = 3  # 369 MB of distinct weights per pass, beyond the host LLC
     mats = []
     for c in range(ncopy):
@@ -518,14 +533,29 @@ def cpu_baseline(seconds):
             L.append((p["W"], p["SB"], p["X"][0], M, K))
         mats.append(L)
     step_bytes = sum(int4_bytes(M, K) for _, M, K in LLAMA)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        for W, SB, X, M, K in mats[n % ncopy]:
-            oracle.int4_gemv_cpu_fast(W, SB, X, M, K, G, nthreads=cores)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
+
+    def timed(path, budget, min_passes):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            for W, SB, X, M, K in mats[n % ncopy]:
+                oracle.int4_gemv_cpu_fast(W, SB, X, M, K, G, nthreads=cores, path=path)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget and n >= min_passes:
+                return n, el
+
+    best = oracle.cpu_fast_path_name(0)
+    paths, probes = [], {}
+    for path in (oracle.CPU_AVX2, oracle.CPU_AVX512, oracle.CPU_FP16):
+        paths.append(path)
+        if oracle.cpu_fast_path_name(path) == best:
             break
+    timed(paths[-1], 0.0, 1)  # thread pool start, first touch
+    for path in paths:
+        n, el = timed(path, 0.5, ncopy)
+        probes[oracle.cpu_fast_path_name(path)] = round(step_bytes * n / el / 1e9, 2)
+    path = max(paths, key=lambda q: probes[oracle.cpu_fast_path_name(q)])
+    n, el = timed(path, seconds, ncopy)
     layer_s = el / n
     # the fp64 oracle (the reference's host check, int4-gemv/src/main.mm:64-92)
     # on the same cores, over a shorter sample of the same layers
@@ -540,11 +570,16 @@ def cpu_baseline(seconds):
     b64 = sum(int4_bytes(*LLAMA[i % len(LLAMA)][1:]) for i in range(n64))
     fp64 = {"value": round(b64 / el64 / 1e9, 3), "unit": "GB/s", "cores": cores,
             "sample": f"{n64} GEMVs of the Llama layer shapes in {el64:.1f} s"}
+    name = oracle.cpu_fast_path_name(path)
     return {"value": round(step_bytes / layer_s / 1e9, 2), "unit": "GB/s", "cores": cores,
             "kind": "port",
             "sample": f"{n} Llama-3-8B layers (7 int4 GEMVs each, {step_bytes / 1e6:.1f} MB) "
-                      f"over {ncopy} weight copies in {el:.1f} s; x86 AVX2+F16C restatement of "
-                      f"cpu_gemv_neon (hetero-gemv/src/cpu_gemv.h:88-103)",
+                      f"over {ncopy} weight copies in {el:.1f} s; {name}, restating "
+                      f"hetero-gemv/src/cpu_gemv.h:55-103, on a persistent pool of {cores} "
+                      f"threads ({affinity} cores in this process's affinity)",
+            "cpu": cpu_model(),
+            "path": name,
+            "path_probe_gbs": probes,
             "ms_per_layer": round(layer_s * 1e3, 3),
             "ms_per_step_32_layers": round(layer_s * 1e3 * N_LAYERS, 2),
             "fp64_oracle": fp64}

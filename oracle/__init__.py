@@ -54,6 +54,9 @@ def lib():
         L.kqref_moe_block_f64.argtypes = [vp, C.POINTER(MoEDesc), vp, i32, vp, i32, u32, vp, vp,
                                           vp, i32]
         L.kqref_int4_gemv_cpu_fast.argtypes = [vp, vp, vp, vp, u32, u32, u32, i32]
+        L.kqref_int4_gemv_cpu_fast_path.argtypes = [vp, vp, vp, vp, u32, u32, u32, i32, i32]
+        L.kqref_cpu_fast_path_name.argtypes = [i32]
+        L.kqref_cpu_fast_path_name.restype = C.c_char_p
         L.kqref_cpu_fast_supported.restype = i32
         L.kqref_vq_quantize.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, C.c_uint64, vp,
                                         vp, vp, vp]
@@ -179,12 +182,21 @@ def cpu_fast_supported():
     return bool(lib().kqref_cpu_fast_supported())
 
 
-def int4_gemv_cpu_fast(W, SB, X, M, K, G, nthreads=0):
+CPU_AVX2, CPU_AVX512, CPU_FP16 = 1, 2, 3
+
+
+def cpu_fast_path_name(path=0):
+    return lib().kqref_cpu_fast_path_name(path).decode()
+
+
+def int4_gemv_cpu_fast(W, SB, X, M, K, G, nthreads=0, path=0):
+    """The reference's CPU int4 GEMV restated for x86 (path 0: the fastest
+    this CPU has; CPU_FP16 = neon16, CPU_AVX512 / CPU_AVX2 = neon fp32)."""
     W = _c(W, np.uint32)
     SB = _c(SB, np.uint16)
     X = _c(X, np.uint16)
     Y = np.zeros(M, np.float32)
-    lib().kqref_int4_gemv_cpu_fast(_p(W), _p(SB), _p(X), _p(Y), M, K, G, nthreads)
+    lib().kqref_int4_gemv_cpu_fast_path(_p(W), _p(SB), _p(X), _p(Y), M, K, G, nthreads, path)
     return Y
 
 

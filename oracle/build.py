@@ -3,8 +3,10 @@
 Compiles oracle/kqref.c (fp64 restatement of the reference CPU paths),
 oracle/vqquant.c (the VQ quantiser as specified for the GPU) and
 oracle/cpu_fast.c (x86 restatement of the reference's CPU int4 GEMV, the timed
-baseline) into oracle/_build/libkqref.so with gcc. No -ffast-math: the oracle
-relies on IEEE fp64 semantics.
+baseline) into oracle/_build/libkqref.so with gcc; cpu_fast.c goes through
+ROCm's clang when it is there, since the neon16 restatement needs the
+AVX-512-FP16 intrinsics that gcc 11 lacks (with gcc it builds without that
+path). No -ffast-math: the oracle relies on IEEE fp64 semantics.
 
 The reference's own CPU code cannot be compiled here (its CPU references sit in
 Objective-C++ translation units that import Metal/Foundation, and its fast
@@ -19,16 +21,24 @@ OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(OUT_DIR, "libkqref.so")
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(OUT_DIR, exist_ok=True)
-    srcs = [os.path.join(HERE, "kqref.c"), os.path.join(HERE, "vqquant.c"),
-            os.path.join(HERE, "cpu_fast.c")]
-    tmp = LIB + ".tmp"
-    cmd = ["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-pthread", "-Wall", "-Wextra",
-           "-Wno-unused-parameter", "-o", tmp] + srcs + ["-lm"]
+CLANG = "/opt/rocm/llvm/bin/clang"
+FLAGS = ["-O2", "-std=c11", "-fPIC", "-pthread", "-Wall", "-Wextra", "-Wno-unused-parameter"]
+
+
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(OUT_DIR, exist_ok=True)
+    fast_cc = CLANG if os.path.exists(CLANG) else "gcc"
+    fast_o = os.path.join(OUT_DIR, "cpu_fast.o")
+    _run([fast_cc] + FLAGS + ["-c", "-o", fast_o, os.path.join(HERE, "cpu_fast.c")], verbose)
+    srcs = [os.path.join(HERE, "kqref.c"), os.path.join(HERE, "vqquant.c")]
+    tmp = LIB + ".tmp"
+    _run(["gcc"] + FLAGS + ["-shared", "-o", tmp] + srcs + [fast_o, "-lm"], verbose)
     os.replace(tmp, LIB)
     return LIB
 

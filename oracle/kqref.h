@@ -94,15 +94,22 @@ void kqref_moe_block_f64(const uint8_t* pool, const kqref_moe_desc* d, const voi
                          const void* X, int x_dtype, uint32_t batch, uint32_t* idx, double* wgt,
                          double* Y, int nthreads);
 
-/* ---- timed CPU baseline (x86 restatement of the reference's CPU int4 path) ----
- * Restates cpu_gemv_neon hetero-gemv/src/cpu_gemv.h:88-103 (32-weight chunk
- * unpack, fp32 multiply-add against x, per-chunk scale/bias fold with xs)
- * with AVX2+F16C+FMA in place of NEON, row blocks over nthreads threads.
+/* ---- timed CPU baseline (x86 restatements of the reference's CPU int4 paths) ----
+ * path 3: cpu_gemv_neon16 hetero-gemv/src/cpu_gemv.h:55-84 (32-weight chunk
+ * unpack, fp16 FMA against fp16 x in 8 lanes, fp32 fold per chunk) on
+ * AVX-512-FP16; path 2 / 1: cpu_gemv_neon cpu_gemv.h:88-103 (fp32 FMA against
+ * fp32 x) on AVX-512F / AVX2+FMA. path <= 0 picks the fastest the CPU has.
+ * Row blocks over a persistent pool of nthreads threads.
  * SB interleaved fp16 (scale, bias); x fp16; y fp32. */
+void kqref_int4_gemv_cpu_fast_path(const uint32_t* W, const uint16_t* SB, const uint16_t* X,
+                                   float* Y, uint32_t M, uint32_t K, uint32_t G, int nthreads,
+                                   int path);
 void kqref_int4_gemv_cpu_fast(const uint32_t* W, const uint16_t* SB, const uint16_t* X,
                               float* Y, uint32_t M, uint32_t K, uint32_t G, int nthreads);
-/* 1 if this CPU has AVX2, FMA and F16C (the fast path's requirement). */
+/* 1 if this CPU has at least AVX2, FMA and F16C (the slowest path's requirement). */
 int kqref_cpu_fast_supported(void);
+/* Name of a path (path <= 0: the fastest this CPU has). */
+const char* kqref_cpu_fast_path_name(int path);
 
 /* VQ quantiser (vqquant.c): quantize_matrix / _kmeans of
  * vq-gemv/quant/pq_quantize.py:28-83 as specified for the GPU quantiser
