@@ -199,14 +199,19 @@ typedef struct kq_moe_desc {
 void kq_moe_default_desc(kq_moe_desc* d);
 
 /* Bytes of workspace the MoE entry points need for `batch` tokens: the router
- * logits, a completion counter, the routing plan (distinct experts and
- * their token slots) that the block's gate/up and down kernels read, and the
- * per-slot down products of the block at 6 or more tokens. A new
- * workspace must be zeroed once with kq_moe_workspace_init (a kernel, not a
- * memset, so it can sit in a captured graph) before its first use; every call
- * leaves it ready for the next. Calls sharing one workspace must be
- * stream-ordered. The standalone gate_up and down derive the plan from idx
- * and accept a NULL workspace. */
+ * logits, a completion counter, the one-launch block's grid-barrier word, the
+ * routing plan (distinct experts and their token slots) that the block's
+ * gate/up and down kernels read, and the per-slot down products of the block
+ * at 6 or more tokens. A new workspace must be zeroed once with
+ * kq_moe_workspace_init (a kernel, not a memset, so it can sit in a captured
+ * graph) before its first use; every call leaves it ready for the next.
+ * Calls sharing one workspace must be stream-ordered. The uint32 at byte
+ * KQ_MOE_WS_ERR_OFFSET stays 0 unless a one-launch block's barrier wait gave
+ * up (all of its workgroups were not resident together, e.g. beside other
+ * work on the GPU): that call's outputs are then invalid, and the word stays
+ * set until the workspace is initialised again. The standalone gate_up and
+ * down derive the plan from idx and accept a NULL workspace. */
+#define KQ_MOE_WS_ERR_OFFSET 128
 size_t kq_moe_workspace_size(const kq_moe_desc* d, uint32_t batch);
 kq_status kq_moe_workspace_init(void* ws, size_t bytes, kq_stream_t stream);
 
@@ -252,6 +257,30 @@ kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d,
                        uint32_t batch, uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H,
                        void* Y, kq_dtype y_dtype, void* ws, size_t ws_bytes,
                        kq_stream_t stream);
+
+/* kq_moe_block with the launch structure chosen (bit-identical results on
+ * every path). KQ_MOE_PATH_AUTO and KQ_MOE_PATH_LAUNCHES: what kq_moe_block
+ * does, the three passes of encodeFused (moe-fused/src/main.mm:176-206).
+ * KQ_MOE_PATH_ONE: one token, the whole block in one launch of one
+ * workgroup per CU (router logits exchanged through tagged device-coherent
+ * stores, h through one grid-wide barrier); about as fast as three launches
+ * inside a graph, two launches fewer for eager callers. Every workgroup must
+ * be resident at once: the path is refused (KQ_EUNSUPPORTED) when the
+ * occupancy query says otherwise, and a wait that still gives up (the GPU
+ * shared with other work) sets the workspace's error word (see
+ * kq_moe_workspace_size). KQ_EUNSUPPORTED too unless batch is 1, hidden and
+ * inter need the same number of 1024-element steps, and each wave's down
+ * rows fit its registers (ceil(ceil(hidden / (2 x CUs)) / floor(8 / top_k))
+ * <= 4, 2 when hidden > 3072). New: the reference always encodes three
+ * passes. */
+#define KQ_MOE_PATH_AUTO 0
+#define KQ_MOE_PATH_LAUNCHES 1
+#define KQ_MOE_PATH_ONE 2
+kq_status kq_moe_block_path(const uint8_t* pool, const kq_moe_desc* d,
+                            const void* R, kq_dtype r_dtype, const void* X, kq_dtype x_dtype,
+                            uint32_t batch, uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H,
+                            void* Y, kq_dtype y_dtype, void* ws, size_t ws_bytes, int path,
+                            kq_stream_t stream);
 
 /* kq_moe_block without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,

@@ -315,16 +315,30 @@ kq_status check_block(const uint8_t* pool, const kq_moe_desc* d, const void* R, 
 }
 }  // namespace
 
+kq_status kq_moe_block_path(const uint8_t* pool, const kq_moe_desc* d, const void* R,
+                            kq_dtype r_dtype, const void* X, kq_dtype x_dtype, uint32_t batch,
+                            uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H, void* Y,
+                            kq_dtype y_dtype, void* ws, size_t ws_bytes, int path,
+                            kq_stream_t stream) {
+    kq_status st = check_block(pool, d, R, r_dtype, X, x_dtype, batch, idx, wgt, xh, H, Y, y_dtype);
+    if (st != KQ_OK) return st;
+    if ((st = check_ws(d, batch, ws, ws_bytes)) != KQ_OK) return st;
+    if (path != KQ_MOE_PATH_AUTO && path != KQ_MOE_PATH_LAUNCHES && path != KQ_MOE_PATH_ONE)
+        return KQ_EINVAL;
+    if (path == KQ_MOE_PATH_ONE &&
+        !kq::moe_one_supported(*d, batch))
+        return KQ_EUNSUPPORTED;
+    return hip_status(kq::launch_moe_block(pool, *d, R, r_dtype == KQ_F32, X, x_dtype == KQ_F32,
+                                           batch, idx, wgt, xh, H, Y, y_dtype == KQ_F32, ws,
+                                           reinterpret_cast<hipStream_t>(stream), path));
+}
+
 kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d, const void* R, kq_dtype r_dtype,
                        const void* X, kq_dtype x_dtype, uint32_t batch, uint32_t* idx, float* wgt,
                        uint16_t* xh, uint16_t* H, void* Y, kq_dtype y_dtype, void* ws,
                        size_t ws_bytes, kq_stream_t stream) {
-    kq_status st = check_block(pool, d, R, r_dtype, X, x_dtype, batch, idx, wgt, xh, H, Y, y_dtype);
-    if (st != KQ_OK) return st;
-    if ((st = check_ws(d, batch, ws, ws_bytes)) != KQ_OK) return st;
-    return hip_status(kq::launch_moe_block(pool, *d, R, r_dtype == KQ_F32, X, x_dtype == KQ_F32,
-                                           batch, idx, wgt, xh, H, Y, y_dtype == KQ_F32, ws,
-                                           reinterpret_cast<hipStream_t>(stream)));
+    return kq_moe_block_path(pool, d, R, r_dtype, X, x_dtype, batch, idx, wgt, xh, H, Y, y_dtype,
+                             ws, ws_bytes, KQ_MOE_PATH_AUTO, stream);
 }
 
 kq_status kq_moe_block_noalloc(const uint8_t* pool, const kq_moe_desc* d, const void* R,

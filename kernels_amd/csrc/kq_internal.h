@@ -83,9 +83,12 @@ hipError_t launch_moe_block_noalloc(const uint8_t* pool, const kq_moe_desc& d, c
                                     bool r_f32, const void* X, bool x_f32, uint32_t batch,
                                     uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H, void* Y,
                                     bool y_f32, hipStream_t s);
+// path: KQ_MOE_PATH_* (KQ_MOE_PATH_ONE only where moe_one_supported holds)
 hipError_t launch_moe_block(const uint8_t* pool, const kq_moe_desc& d, const void* R, bool r_f32,
                             const void* X, bool x_f32, uint32_t batch, uint32_t* idx, float* wgt,
                             uint16_t* xh, uint16_t* H, void* Y, bool y_f32, void* ws,
-                            hipStream_t s);
+                            hipStream_t s, int path);
+// The one-launch block's limits (shape, and every workgroup resident at once).
+bool moe_one_supported(const kq_moe_desc& d, uint32_t batch);
 
 }  // namespace kq

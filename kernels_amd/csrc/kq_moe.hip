@@ -79,22 +79,31 @@ struct Plan {
 };
 
 struct WsLayout {
-    size_t lg, cnt, plan, ys, total;
+    size_t lg, cnt, plan, sync, tag, ys, total;
 };
 
-// Workspace: [completion counter][plan][logits f32 batch x n_experts]
-// [per-slot down products f32 batch x top_k x hidden]. The counter and the
-// plan sit at fixed offsets, the same for every batch and descriptor: a
-// workspace sized for a large batch and reused at a smaller one (or the
-// reverse) never has its counter or plan overwritten by another call's
-// logits or products. Every call writes the logits and products it reads.
+// Workspace: [completion counter, error word][plan][grid-barrier counters]
+// [tagged logits of the one-launch block, kTagCopies x 8 B x 256][logits f32 batch x
+// n_experts][per-slot down products f32 batch x top_k x hidden]. Everything
+// before the logits sits at fixed offsets, the same for every batch and
+// descriptor: a workspace sized for a large batch and reused at a smaller
+// one (or the reverse) never has its counter, plan or barrier state
+// overwritten by another call's logits or products. Every call writes the
+// logits and products it reads.
 constexpr size_t kWsCnt = 0, kWsPlan = 256;
+constexpr uint32_t kSyncGroups = 32;  // barrier counters: workgroups b % 32 (8 per counter at 256)
+constexpr size_t kSyncStride = 256;  // bytes between counters (separate lines)
+constexpr size_t kWsSync = (kWsPlan + sizeof(Plan) + 255) & ~(size_t)255;
+constexpr size_t kWsTag = kWsSync + kSyncGroups * kSyncStride;
+constexpr uint32_t kTagCopies = 8;  // one per XCD (workgroups b % 8)
 WsLayout ws_layout(const kq_moe_desc& d, uint32_t batch) {
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
     WsLayout L;
     L.cnt = kWsCnt;
     L.plan = kWsPlan;
-    L.lg = al(L.plan + sizeof(Plan));
+    L.sync = kWsSync;
+    L.tag = kWsTag;
+    L.lg = L.tag + kTagCopies * 8 * 256;
     L.ys = L.lg + al(4ull * batch * d.n_experts);
     L.total = L.ys + al(4ull * batch * d.top_k * d.hidden);
     return L;
@@ -151,21 +160,31 @@ __device__ __forceinline__ void unpack8(const Raw8<F32>& r, float v[8]) {
 // the softmax of the selected logits. COHERENT: the logits come from other
 // workgroups of the same launch (device-coherent loads); otherwise from an
 // earlier launch (plain loads).
+// topk_vals: the same from the logits already in registers (lane l holds
+// experts l + 64q in x[q]).
+__device__ __forceinline__ void topk_vals(const float (&x)[4], uint32_t NE, uint32_t TK,
+                                          uint32_t* idx_out, float* wgt_out);
 template <bool COHERENT>
 __device__ __forceinline__ void topk_wave(const float* L, uint32_t NE, uint32_t TK,
                           uint32_t* idx_out, float* wgt_out) {
     const uint32_t lane = threadIdx.x & 63;
-    float v[4];
+    float x[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t ei = lane + 64 * q;
-        float x;
         if constexpr (COHERENT)
-            x = __hip_atomic_load(L + min(ei, NE - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            x[q] = __hip_atomic_load(L + min(ei, NE - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else
-            x = L[min(ei, NE - 1)];
-        v[q] = cand(x, ei < NE);
+            x[q] = L[min(ei, NE - 1)];
     }
+    topk_vals(x, NE, TK, idx_out, wgt_out);
+}
+__device__ __forceinline__ void topk_vals(const float (&x)[4], uint32_t NE, uint32_t TK,
+                                          uint32_t* idx_out, float* wgt_out) {
+    const uint32_t lane = threadIdx.x & 63;
+    float v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = cand(x[q], lane + 64 * q < NE);
     float chosen[kMaxTopK];
     uint32_t pick[kMaxTopK];
     topk_select(v, TK, pick, chosen);
@@ -451,12 +470,14 @@ __device__ void get_plan(const Plan* plan_g, const uint32_t* idx, const float* w
 // launch reads the same plan, so any fixed order gives the same result):
 // at one token the top-k experts are distinct and slot s is plan entry s.
 // At most kPlanSlots slots (the launcher's limit), lane s takes slot s.
+// COHERENT: the logits were written by other workgroups of the same launch.
 constexpr uint32_t kPlanSlots = 2 * kMaxTopK;
+template <bool COHERENT = false>
 __device__ __forceinline__ void plan_from_logits(const float* lg, uint32_t batch, uint32_t NE, uint32_t TK,
                                  Plan& ps, uint32_t* s_idx, float* s_wgt) {
     const uint32_t lane = threadIdx.x & 63;
     for (uint32_t t = 0; t < batch; ++t)
-        topk_wave<false>(lg + (size_t)t * NE, NE, TK, s_idx + t * TK, s_wgt + t * TK);
+        topk_wave<COHERENT>(lg + (size_t)t * NE, NE, TK, s_idx + t * TK, s_wgt + t * TK);
     __builtin_amdgcn_wave_barrier();
     const uint32_t nslots = batch * TK;
     const uint32_t e = lane < nslots ? min(s_idx[lane], NE - 1) : 0xFFFFFFFFu;
@@ -720,11 +741,14 @@ __device__ __forceinline__ void st_issue(StSlot<J>& e, rsrc_t r, const StLane<J>
 
 // Activation staging, part 1: every load of nvec fp16 vectors of K elements
 // (vector v at src + v * K), issued before the ring so the waits that finish
-// the staging never wait for weights.
+// the staging never wait for weights. AUX: the loads' cache policy (kCoh:
+// device-coherent, for vectors other workgroups of the same launch wrote).
 struct StStage {
     u32x4 sv[kStXr];
     uint32_t total;
 };
+constexpr int kCoh = 16;  // sc1: agent-scope coherent access
+template <int AUX = 0>
 __device__ __forceinline__ void st_stage_load(StStage& st, const uint16_t* src, uint32_t nvec,
                                               uint32_t K) {
     const uint32_t nthr = blockDim.x, tid = threadIdx.x;
@@ -734,31 +758,31 @@ __device__ __forceinline__ void st_stage_load(StStage& st, const uint16_t* src, 
     for (int i = 0; i < kStXr; ++i) {
         if ((uint32_t)i * nthr >= st.total) break;  // uniform
         const uint32_t w = i * nthr + tid;
-        st.sv[i] = __builtin_amdgcn_raw_buffer_load_b128(r, w < st.total ? w * 16 : kStOOB, 0, 0);
+        st.sv[i] = __builtin_amdgcn_raw_buffer_load_b128(r, w < st.total ? w * 16 : kStOOB, 0, AUX);
     }
 }
 // Part 2: permuted pairs and chunk constants into the LDS blocks
 // [(v * J + j) * kABlk]: planes jw at jw * 512 + c0 * 16, (sum, const) at
 // 2048 + c0 * 8; chunks past K are zero. The caller synchronises.
+// st_word_store: word w (8 elements) of the staged vectors, every lane of
+// the wave taking part (quad sums), the store only if w < total.
 template <int J>
-__device__ __forceinline__ void st_stage_store(const StStage& st, unsigned char* act, uint32_t nvec,
-                                               uint32_t K) {
-    const uint32_t nthr = blockDim.x, tid = threadIdx.x, nw = K >> 3, nch = K >> 5;
-#pragma unroll
-    for (int i = 0; i < kStXr; ++i) {
-        if ((uint32_t)i * nthr >= st.total) break;  // uniform
-        const uint32_t w = i * nthr + tid;
-        float s, c;
-        word_consts(st.sv[i], s, c);
-        s = quad_sum(s);
-        c = quad_sum(c);
-        if (w < st.total) {
-            const uint32_t v = w / nw, wi = w - v * nw, ch = wi >> 2, jw = wi & 3;
-            unsigned char* blk = act + (v * J + (ch >> 5)) * kABlk;
-            *reinterpret_cast<u32x4*>(blk + jw * 512 + (ch & 31) * 16) = pair_perm(st.sv[i]);
-            if (jw == 0) *reinterpret_cast<float2*>(blk + 2048 + (ch & 31) * 8) = make_float2(s, c);
-        }
+__device__ __forceinline__ void st_word_store(const u32x4& sv, uint32_t w, uint32_t total,
+                                              unsigned char* act, uint32_t nw) {
+    float s, c;
+    word_consts(sv, s, c);
+    s = quad_sum(s);
+    c = quad_sum(c);
+    if (w < total) {
+        const uint32_t v = w / nw, wi = w - v * nw, ch = wi >> 2, jw = wi & 3;
+        unsigned char* blk = act + (v * J + (ch >> 5)) * kABlk;
+        *reinterpret_cast<u32x4*>(blk + jw * 512 + (ch & 31) * 16) = pair_perm(sv);
+        if (jw == 0) *reinterpret_cast<float2*>(blk + 2048 + (ch & 31) * 8) = make_float2(s, c);
     }
+}
+template <int J>
+__device__ __forceinline__ void st_pad_store(unsigned char* act, uint32_t nvec, uint32_t K) {
+    const uint32_t nthr = blockDim.x, tid = threadIdx.x, nch = K >> 5;
     const uint32_t npad = 32 * J - nch;
     for (uint32_t i = tid; i < nvec * 5 * npad; i += nthr) {
         const uint32_t v = i / (5 * npad), rem = i - v * 5 * npad, jw = rem / npad;
@@ -767,6 +791,17 @@ __device__ __forceinline__ void st_stage_store(const StStage& st, unsigned char*
         if (jw < 4) *reinterpret_cast<u32x4*>(blk + jw * 512 + (ch & 31) * 16) = u32x4{0, 0, 0, 0};
         else *reinterpret_cast<float2*>(blk + 2048 + (ch & 31) * 8) = make_float2(0.0f, 0.0f);
     }
+}
+template <int J>
+__device__ __forceinline__ void st_stage_store(const StStage& st, unsigned char* act, uint32_t nvec,
+                                               uint32_t K) {
+    const uint32_t nthr = blockDim.x, tid = threadIdx.x, nw = K >> 3;
+#pragma unroll
+    for (int i = 0; i < kStXr; ++i) {
+        if ((uint32_t)i * nthr >= st.total) break;  // uniform
+        st_word_store<J>(st.sv[i], i * nthr + tid, st.total, act, nw);
+    }
+    st_pad_store<J>(act, nvec, K);
 }
 
 // The dequantised words of one row pair (token-independent).
@@ -1436,6 +1471,426 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_part_k(
 }
 
 // Y[t][m] = sum over k of ys[t * TK + k][m], in k order.
+// ---------------------------------------------------------------------------
+// 4. One-launch block (one token, KQ_MOE_PATH_ONE): router logits, top-k,
+//    gate/up + SwiGLU and down + combine in a single launch of one 8-wave
+//    workgroup per CU, with the three-launch block's results bit for bit.
+//    The three-launch block pays two kernel boundaries and a plan read at
+//    the start of each later launch. Measured at gpt-oss-120b shapes (12
+//    layers, graph replays, same process): 21.87 us per block vs 21.94 us
+//    for three launches -- the phase boundaries inside the launch (logit
+//    exchange ~2.5 us, grid barrier ~1 us plus the down stream) cost about
+//    what the kernel boundaries do, so the block stays on three launches by
+//    default; this path saves two launches for callers that launch eagerly.
+//    Streaming the down weights with gate/up (issued up front, or one item
+//    per gate/up step) and deeper gate/up rings (3, 4: 22.19, 23.47 us) were
+//    slower: the gate/up stream already runs at ~6.9 TB/s.
+//    Here:
+//    - each router wave stores its logit together with a tag (the call's
+//      sequence number + 1) as one 8-byte device-coherent store, and wave 0
+//      of every workgroup polls the tagged logits until all carry this
+//      call's tag, then runs the top-k: the logits are their own barrier;
+//    - each workgroup issues its share of the down rows into registers as
+//      soon as its gate/up ring is primed, so the down weights stream with
+//      gate/up;
+//    - h goes to memory with device-coherent stores, one grid barrier
+//      follows, and each wave loads the one h vector its down rows need
+//      straight into registers (no LDS staging: down is one expert per wave,
+//      two waves per expert at top-4).
+//    x comes straight from memory into registers too.
+//
+//    Grid barrier: kSyncGroups 64-bit counters that only ever grow, one per
+//    group of workgroups b % kSyncGroups, on separate lines: atomics on one
+//    location are done in turn (measured per barrier at 256 workgroups: one
+//    counter 3.7 us, 8 counters 2.0 us, 32 counters 1.0 us).
+//    A workgroup arrives with one atomic add on its group's counter once its
+//    device-coherent stores have completed; the value it gets back gives the
+//    barrier round r (old / group size), and it waits until every counter
+//    has reached (r + 1) x its group's size, polling all of them with one
+//    load per lane. The round before a workgroup's own arrival is the call's
+//    sequence number (its group cannot complete a round without it), which
+//    gives the logit tag. The launch is sized so that all of its workgroups
+//    are resident at once (one per CU, the occupancy query checked before the
+//    first launch); every poll still gives up after kSpinTicks of the 100 MHz
+//    real-time clock and sets the workspace's error word, so every wave
+//    finishes.
+// ---------------------------------------------------------------------------
+constexpr size_t kWsErr = KQ_MOE_WS_ERR_OFFSET;  // head word (the plan is at 256)
+constexpr uint64_t kSpinTicks = 10000000ull;     // 100 ms
+// down items a wave holds in registers (2 at J = 4, within 256 VGPRs)
+__host__ __device__ constexpr int one_dn(int J) { return J >= 4 ? 2 : 4; }
+constexpr int kOneD = 2;  // gate/up ring depth
+
+__device__ __forceinline__ uint32_t sync_gsize(uint32_t G, uint32_t g) {
+    return G / kSyncGroups + (g < G % kSyncGroups ? 1u : 0u);
+}
+__device__ __forceinline__ void spin_fail(uint32_t* err) {
+    if ((threadIdx.x & 63) == 0)
+        __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Arrival (thread 0, for the workgroup; the caller has made every thread's
+// coherent stores complete and synchronised the workgroup) and wait, split
+// so that work can be issued in between; the value the arrival returns goes
+// to the wait.
+__device__ __forceinline__ uint64_t grid_arrive(unsigned char* sync) {
+    uint64_t old = 0;
+    if (threadIdx.x == 0)
+        old = __hip_atomic_fetch_add(
+            reinterpret_cast<uint64_t*>(sync + (blockIdx.x % kSyncGroups) * kSyncStride), 1ull,
+            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return old;
+}
+__device__ __forceinline__ void grid_wait(unsigned char* sync, uint32_t* err, uint64_t old) {
+    if (threadIdx.x < 64) {  // wave 0 waits for the workgroup
+        const uint32_t G = gridDim.x, lane = threadIdx.x, grp = blockIdx.x % kSyncGroups;
+        const uint64_t old0 = ((uint64_t)__builtin_amdgcn_readlane((uint32_t)(old >> 32), 0) << 32) |
+                              __builtin_amdgcn_readlane((uint32_t)old, 0);
+        const uint64_t round = old0 / sync_gsize(G, grp);
+        const bool mine = lane < kSyncGroups && sync_gsize(G, lane) > 0;
+        const uint64_t target = (round + 1) * (mine ? sync_gsize(G, lane) : 0u);
+        const uint64_t* cnt =
+            reinterpret_cast<const uint64_t*>(sync + (mine ? lane : 0) * kSyncStride);
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (true) {
+            bool done = true;
+            if (mine)
+                done = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target;
+            if (__ballot(!done) == 0) break;
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
+                spin_fail(err);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
+}
+
+// The J chunks of a K-element fp16 vector that lane c0 = lane % 32 uses
+// (chunks c0 + 32j), loaded from memory into the register form st_xload
+// gives (permuted pairs, chunk sum and offset constant; chunks past K zero).
+// F32: the vector is fp32, rounded to fp16 here. AUX: cache policy of the
+// loads. The chunk constants add the four words' constants as
+// (w0 + w1) + (w2 + w3), the order of the staged form's quad sums.
+template <int J, bool F32, int AUX>
+__device__ __forceinline__ void st_xload_mem(StX<J>& x, const void* src, uint32_t K) {
+    const uint32_t c0 = threadIdx.x & 31, nch = K >> 5;
+    const rsrc_t r = make_rsrc(src, K * (F32 ? 4 : 2));
+    u32x4 raw[J][4];
+    f32x4 rf[F32 ? J : 1][F32 ? 8 : 1];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint32_t ch = c0 + 32 * j;
+#pragma unroll
+        for (int jw = 0; jw < 4; ++jw) {
+            if constexpr (F32) {
+                const uint32_t o = ch < nch ? ch * 128 + jw * 32 : kStOOB;
+                rf[j][2 * jw] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, AUX));
+                rf[j][2 * jw + 1] =
+                    __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o + 16, 0, AUX));
+            } else {
+                raw[j][jw] = __builtin_amdgcn_raw_buffer_load_b128(r, ch < nch ? ch * 64 + jw * 16 : kStOOB,
+                                                                   0, AUX);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        float sw[4], cw[4];
+#pragma unroll
+        for (int jw = 0; jw < 4; ++jw) {
+            if constexpr (F32) {
+                const f32x4 a = rf[j][2 * jw], b = rf[j][2 * jw + 1];
+                raw[j][jw] = u32x4{(uint32_t)f2h(a.x) | ((uint32_t)f2h(a.y) << 16),
+                                   (uint32_t)f2h(a.z) | ((uint32_t)f2h(a.w) << 16),
+                                   (uint32_t)f2h(b.x) | ((uint32_t)f2h(b.y) << 16),
+                                   (uint32_t)f2h(b.z) | ((uint32_t)f2h(b.w) << 16)};
+            }
+            word_consts(raw[j][jw], sw[jw], cw[jw]);
+            x.p[j][jw] = pair_perm(raw[j][jw]);
+        }
+        x.k[j] = make_float2((sw[0] + sw[1]) + (sw[2] + sw[3]), (cw[0] + cw[1]) + (cw[2] + cw[3]));
+    }
+}
+
+// The register form from the raw words st_xload_mem loads (fp16 vectors).
+template <int J>
+__device__ __forceinline__ void st_xregs(StX<J>& x, const u32x4 (&raw)[J][4]) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        float sw[4], cw[4];
+#pragma unroll
+        for (int jw = 0; jw < 4; ++jw) {
+            word_consts(raw[j][jw], sw[jw], cw[jw]);
+            x.p[j][jw] = pair_perm(raw[j][jw]);
+        }
+        x.k[j] = make_float2((sw[0] + sw[1]) + (sw[2] + sw[3]), (cw[0] + cw[1]) + (cw[2] + cw[3]));
+    }
+}
+
+// J: chunks per half-wave lane of both projections (hidden and inter of the
+// same J); the router reads hidden in IT = 2J steps of 512 (IT * 512 >= hidden).
+// rf32 / xf32: router weights / x in fp32 (uniform branches).
+template <int J>
+__global__ __launch_bounds__(64 * kStWaves) void moe_one_k(
+    const uint8_t* __restrict__ pool, kq_moe_desc d, const void* __restrict__ R, int rf32,
+    const void* __restrict__ X, int xf32, uint32_t* __restrict__ idx_out,
+    float* __restrict__ wgt_out, uint16_t* __restrict__ xh, uint16_t* H, void* __restrict__ Y,
+    int y_f32, unsigned char* sync, uint64_t* tagged, uint32_t* err, uint32_t pp) {
+    extern __shared__ __align__(16) unsigned char act[];  // ys [top_k][2 pp]
+    __shared__ Plan ps;
+    __shared__ uint32_t s_idx[kMaxSlots];
+    __shared__ float s_wgt[kMaxSlots];
+    constexpr int IT = 2 * J;
+    const uint32_t HID = d.hidden, IN = d.inter, TK = d.top_k, NE = d.n_experts, G = gridDim.x;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6), half = lane >> 5;
+
+    // 1. router logits: expert e in wave e / G of workgroup e % G (spread over
+    // the CUs), with the arithmetic of moe_router_k (the three-launch
+    // block's logits); its loads go first, then the call's sequence number
+    // (this workgroup's barrier counter), then x for gate/up
+    const uint32_t e = wave * G + blockIdx.x;
+    const uint32_t grp = blockIdx.x % kSyncGroups;
+    const uint64_t* seq = reinterpret_cast<const uint64_t*>(sync + grp * kSyncStride);
+    const bool router = e < NE;  // uniform
+    u32x4 rr[IT][2], rx[IT][2];  // 8 router / x elements as loaded (fp32: two words)
+    uint64_t seqv = 0;
+    if (router) {
+#pragma unroll
+        for (int i = 0; i < IT; ++i) {
+            const uint32_t k = min((lane + 64 * i) * 8, HID - 8);
+            if (rf32) {
+                const u32x4* q = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(R) +
+                                                                (size_t)e * HID + k);
+                rr[i][0] = q[0];
+                rr[i][1] = q[1];
+            } else {
+                rr[i][0] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(R) +
+                                                           (size_t)e * HID + k);
+            }
+            if (xf32) {
+                const u32x4* q = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(X) + k);
+                rx[i][0] = q[0];
+                rx[i][1] = q[1];
+            } else {
+                rx[i][0] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(X) + k);
+            }
+        }
+    }
+    if (router || wave == 0) seqv = __hip_atomic_load(seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t tag = (uint32_t)(seqv / sync_gsize(G, grp)) + 1u;
+    if (router) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < IT; ++i) {
+            if ((lane + 64 * i) * 8 < HID) {
+                float rv[8], xv[8];
+                if (rf32) unpack8<true>(Raw8<true>{__builtin_bit_cast(f32x4, rr[i][0]),
+                                                   __builtin_bit_cast(f32x4, rr[i][1])}, rv);
+                else unpack8<false>(Raw8<false>{rr[i][0]}, rv);
+                if (xf32) unpack8<true>(Raw8<true>{__builtin_bit_cast(f32x4, rx[i][0]),
+                                                   __builtin_bit_cast(f32x4, rx[i][1])}, xv);
+                else unpack8<false>(Raw8<false>{rx[i][0]}, xv);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) acc = fmaf(rv[q], xv[q], acc);
+            }
+        }
+        const float v = wave_sum(acc);
+        const uint64_t tv = ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, v);
+        // one copy per XCD: the polls of each XCD's workgroups read their own
+        if (lane < kTagCopies)
+            __hip_atomic_store(tagged + lane * 256 + e, tv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (xf32 && xh)  // xh = half(X), spread over the grid
+        for (uint32_t i = blockIdx.x * blockDim.x + tid; i < HID; i += G * blockDim.x)
+            xh[i] = f2h(reinterpret_cast<const float*>(X)[i]);
+
+    // 2. wave 0: wait for every logit of this call, top-k, the plan (one
+    // token: the top-k experts are distinct, plan entry u is slot u)
+    if (wave == 0) {
+        const uint64_t* mine = tagged + (blockIdx.x % kTagCopies) * 256;
+        float lv[4];
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (true) {
+            uint64_t t[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)  // all four loads in flight at once
+                t[q] = __hip_atomic_load(mine + min(lane + 64 * q, NE - 1), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+            bool done = true;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                lv[q] = __builtin_bit_cast(float, (uint32_t)t[q]);
+                done = done && (uint32_t)(t[q] >> 32) == tag;
+            }
+            if (__ballot(!done) == 0) break;
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
+                spin_fail(err);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        topk_vals(lv, NE, TK, s_idx, s_wgt);
+        __builtin_amdgcn_wave_barrier();
+        if (lane < TK) {
+            ps.expert[lane] = min(s_idx[lane], NE - 1);
+            ps.mask[lane][0] = 1ull << lane;
+            ps.mask[lane][1] = 0;
+        }
+        if (lane == 0) ps.n = TK;
+        if (blockIdx.x == 0 && lane < TK) {
+            idx_out[lane] = s_idx[lane];
+            wgt_out[lane] = s_wgt[lane];
+        }
+    }
+    __syncthreads();
+    const uint32_t nexp = TK;
+    // x (fp16) for gate/up, issued before any weight load (no later wait for
+    // it waits for weights) and after the router's loads (not competing)
+    const uint32_t c0 = lane & 31, nch = HID >> 5;
+    u32x4 xraw[J][4];
+    if (!xf32) {
+        const rsrc_t r = make_rsrc(X, HID * 2);
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int jw = 0; jw < 4; ++jw) {
+                const uint32_t ch = c0 + 32 * j;
+                xraw[j][jw] =
+                    __builtin_amdgcn_raw_buffer_load_b128(r, ch < nch ? ch * 64 + jw * 16 : kStOOB, 0, 0);
+            }
+    }
+
+    // 3. gate/up items (u, row i), u-major, a contiguous range per workgroup,
+    // every kStWaves-th item per wave (moe_gu_stream_k's order)
+    const uint32_t N = nexp * IN;
+    const uint32_t per = (N + G - 1) / G, k0 = blockIdx.x * per;
+    const uint32_t cnt = k0 < N ? min(per, N - k0) : 0;
+    const uint32_t nit = cnt > wave ? (cnt - wave + kStWaves - 1) / kStWaves : 0;
+    const uint32_t rowb = HID >> 1, metab = (HID >> 6) * 2;
+    const StLane<J> L = st_lane<J>(half ? d.off_up : d.off_gate, d, HID, 0, 0, 0);
+    constexpr int D = kOneD;
+    StSlot<J> ring[D];
+    struct Cur {
+        uint32_t u, i;
+    };
+    auto adv = [&](Cur& c) __attribute__((always_inline)) {
+        c.i += kStWaves;
+        while (c.i >= IN) {  // uniform
+            c.i -= IN;
+            ++c.u;
+        }
+    };
+    Cur ci{(k0 + wave) / IN, (k0 + wave) % IN}, cc = ci, clast = ci;
+    uint32_t nis = 0;
+    auto issue = [&](StSlot<J>& sl) __attribute__((always_inline)) {
+        if (nis < nit) clast = ci;  // padding re-reads the last item
+        const uint32_t ex = __builtin_amdgcn_readfirstlane(ps.expert[min(clast.u, nexp - 1)]);
+        const rsrc_t r = make_rsrc(pool + (size_t)ex * d.blob, (uint32_t)d.blob);
+        const uint32_t i = __builtin_amdgcn_readfirstlane(clast.i);
+        st_issue<J>(sl, r, L, i * rowb, i * metab, i * 2);
+        adv(ci);
+        ++nis;
+    };
+#pragma unroll
+    for (int q = 0; q < D; ++q) {
+        issue(ring[q]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // 4. down items: wave q takes expert u = q % top_k and, among the W_u
+    // waves of u, rank q / top_k: output row pairs p0 + rank + k W_u of this
+    // workgroup's [p0, p0 + np), loaded into registers between the grid
+    // barrier's arrival and its wait; items past the end load out of range
+    // (no traffic)
+    const uint32_t npairs = HID >> 1, p0 = blockIdx.x * pp;
+    const uint32_t np = p0 < npairs ? min(pp, npairs - p0) : 0;
+    const uint32_t du = wave % TK, drank = wave / TK;
+    const uint32_t dW = kStWaves / TK + (du < kStWaves % TK ? 1u : 0u);
+    const uint32_t rowd = IN >> 1, metad = (IN >> 6) * 2;
+    const StLane<J> Ld = st_lane<J>(d.off_down, d, IN, half * rowd, half * metad, half * 2);
+    const uint32_t dex = __builtin_amdgcn_readfirstlane(ps.expert[du]);
+    constexpr int DN = one_dn(J);
+    StSlot<J> dn[DN];
+    auto issue_dn = [&](int k) __attribute__((always_inline)) {
+        const uint32_t pi = drank + dW * k;
+        const bool ok = pi < np;  // uniform
+        const uint32_t p = p0 + (ok ? pi : 0);
+        const rsrc_t r = make_rsrc(pool + (size_t)dex * d.blob, ok ? (uint32_t)d.blob : 0u);
+        st_issue<J>(dn[k], r, Ld, 2 * p * rowd, 2 * p * metad, 2 * p * 2);
+    };
+
+    // x into registers
+    StX<J> xr;
+    if (xf32) st_xload_mem<J, true, 0>(xr, X, HID);
+    else st_xregs<J>(xr, xraw);
+
+    const DequantConsts kc;
+    // every lane stores the step's h (the same value and address): a fixed
+    // store count per step, device-coherent for the down phase's loads
+    auto step = [&](const StSlot<J>& sl, uint32_t it, bool tail) __attribute__((always_inline)) {
+        if (tail && it >= nit) return;  // padding (uniform)
+        const float2 hs = half_sums(st_dotx_dq<J>(sl, kc, xr));
+        const float bg = bf2f((uint16_t)__builtin_amdgcn_readlane(sl.bi, 0));
+        const float bu = bf2f((uint16_t)__builtin_amdgcn_readlane(sl.bi, 32));
+        const uint16_t hv = f2h(swiglu(hs.x + bg, hs.y + bu));
+        __hip_atomic_store(H + (size_t)cc.u * IN + cc.i, hv, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        adv(cc);
+    };
+    const uint32_t nsteps = (nit + D - 1) / D * D;
+    uint32_t it = 0;
+    for (; it + D < nsteps; it += D) {
+#pragma unroll
+        for (int q = 0; q < D; ++q) {
+            step(ring[q], it + q, false);
+            issue(ring[q]);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < D; ++q) step(ring[q], it + q, true);
+    // every wave's h stores complete, the workgroup arrives, then the down
+    // loads go out (their fetch overlaps the wait)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const uint64_t ticket = grid_arrive(sync);
+#pragma unroll
+    for (int k = 0; k < DN; ++k) issue_dn(k);
+
+    __builtin_amdgcn_sched_barrier(0);
+    grid_wait(sync, err, ticket);
+
+    // 5. the wave's h vector (device-coherent loads) into registers, down
+    // items, per-slot products to LDS, then the combine
+    StX<J> hx;
+    st_xload_mem<J, false, kCoh>(hx, H + (size_t)du * IN, IN);
+    float* ys = reinterpret_cast<float*>(act);  // [TK][2 * pp]
+    const float wt = s_wgt[du];
+#pragma unroll
+    for (int k = 0; k < DN; ++k) {
+        const uint32_t pi = drank + dW * k;
+        if (pi >= np) break;  // uniform
+        const float2 hs = half_sums(st_dotx_dq<J>(dn[k], kc, hx));
+        const float b0 = bf2f((uint16_t)__builtin_amdgcn_readlane(dn[k].bi, 0));
+        const float b1 = bf2f((uint16_t)__builtin_amdgcn_readlane(dn[k].bi, 32));
+        if (lane == 0) {
+            ys[du * 2 * pp + 2 * pi] = wt * (hs.x + b0);
+            ys[du * 2 * pp + 2 * pi + 1] = wt * (hs.y + b1);
+        }
+    }
+    __syncthreads();
+    // combine in slot order (moe-fused/src/kernels.metal:254-263)
+    for (uint32_t i = tid; i < 2 * np; i += blockDim.x) {
+        float acc = 0.0f;
+        for (uint32_t q = 0; q < TK; ++q) acc += ys[q * 2 * pp + i];
+        const uint32_t m = 2 * p0 + i;
+        if (y_f32) reinterpret_cast<float*>(Y)[m] = acc;
+        else reinterpret_cast<uint16_t*>(Y)[m] = f2h(acc);
+    }
+}
+
 __global__ __launch_bounds__(256) void moe_combine_k(const float* __restrict__ ys, void* Y,
                                                      int y_f32, uint32_t batch, uint32_t TK,
                                                      uint32_t HID) {
@@ -1718,6 +2173,84 @@ hipError_t launch_dn(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* 
     return hipGetLastError();
 }
 
+// One-launch block limits: one token; hidden and inter of one chunk count
+// per lane; every wave's down items within its registers; the router's
+// experts within the grid's waves.
+uint32_t one_pp(const kq_moe_desc& d) {
+    const uint32_t G = cu_count();
+    return (d.hidden / 2 + G - 1) / G;
+}
+size_t one_lds(const kq_moe_desc& d) { return (size_t)d.top_k * 2 * one_pp(d) * 4; }
+bool one_fits(const kq_moe_desc& d, uint32_t batch) {
+    const uint32_t J = chunks_j(d.hidden);
+    if (batch != 1 || J < 1 || J > 4 || chunks_j(d.inter) != J || cu_count() >= 0x10000u)
+        return false;
+    const uint32_t wmin = (uint32_t)kStWaves / d.top_k;  // waves per expert (top_k <= 8)
+    return wmin >= 1 && (one_pp(d) + wmin - 1) / wmin <= (uint32_t)one_dn((int)J) &&
+           d.n_experts <= cu_count() * (uint32_t)kStWaves && d.blob < (1ull << 31) &&
+           one_lds(d) + kStStatic <= kLdsMax;
+}
+const void* one_kern(uint32_t J) {
+    switch (J) {
+        case 1: return reinterpret_cast<const void*>(moe_one_k<1>);
+        case 2: return reinterpret_cast<const void*>(moe_one_k<2>);
+        case 3: return reinterpret_cast<const void*>(moe_one_k<3>);
+        case 4: return reinterpret_cast<const void*>(moe_one_k<4>);
+        default: return nullptr;
+    }
+}
+
+// Every workgroup of the launch (one per CU) resident at once: the occupancy
+// query, once per (device, kernel, LDS size).
+struct OneRes {
+    int dev;
+    const void* kern;
+    size_t lds;
+    bool ok;
+};
+std::mutex g_one_mu;
+OneRes g_one_res[64];
+int g_one_n = 0;
+bool one_resident(const void* kern, size_t lds) {
+    int dev = 0;
+    if (kern == nullptr || hipGetDevice(&dev) != hipSuccess) return false;
+    std::lock_guard<std::mutex> lk(g_one_mu);
+    for (int i = 0; i < g_one_n; ++i)
+        if (g_one_res[i].dev == dev && g_one_res[i].kern == kern && g_one_res[i].lds == lds)
+            return g_one_res[i].ok;
+    int nb = 0;
+    const bool ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 64 * kStWaves, lds) ==
+                        hipSuccess &&
+                    nb >= 1;
+    if (g_one_n < 64) g_one_res[g_one_n++] = OneRes{dev, kern, lds, ok};
+    return ok;
+}
+
+template <int J>
+hipError_t go_one(const uint8_t* pool, const kq_moe_desc& d, const void* R, bool rf,
+                  const void* X, bool xf, uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H,
+                  void* Y, bool y_f32, uint8_t* w, const WsLayout& L, hipStream_t s) {
+    auto kern = moe_one_k<J>;
+    const size_t lds = one_lds(d);
+    const hipError_t e = st_lds(kern, lds);
+    if (e != hipSuccess) return e;
+    kern<<<cu_count(), 64 * kStWaves, lds, s>>>(
+        pool, d, R, rf ? 1 : 0, X, xf ? 1 : 0, idx, wgt, xh, H, Y, y_f32 ? 1 : 0, w + L.sync,
+        reinterpret_cast<uint64_t*>(w + L.tag), reinterpret_cast<uint32_t*>(w + kWsErr), one_pp(d));
+    return hipGetLastError();
+}
+hipError_t launch_one(const uint8_t* pool, const kq_moe_desc& d, const void* R, bool rf,
+                      const void* X, bool xf, uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H,
+                      void* Y, bool y_f32, uint8_t* w, const WsLayout& L, hipStream_t s) {
+    switch (chunks_j(d.hidden)) {
+        case 1: return go_one<1>(pool, d, R, rf, X, xf, idx, wgt, xh, H, Y, y_f32, w, L, s);
+        case 2: return go_one<2>(pool, d, R, rf, X, xf, idx, wgt, xh, H, Y, y_f32, w, L, s);
+        case 3: return go_one<3>(pool, d, R, rf, X, xf, idx, wgt, xh, H, Y, y_f32, w, L, s);
+        case 4: return go_one<4>(pool, d, R, rf, X, xf, idx, wgt, xh, H, Y, y_f32, w, L, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 // Per-device address of `scratch`, looked up once per device (with that
 // device current) at the first kq_moe_block_noalloc call on it. The zero
 // fill at set-up is a kernel on the caller's stream (graph-safe), ahead of
@@ -1745,6 +2278,10 @@ hipError_t scratch_ptr(void** out, hipStream_t s) {
 
 }  // namespace
 
+bool moe_one_supported(const kq_moe_desc& d, uint32_t batch) {
+    return one_fits(d, batch) && one_resident(one_kern(chunks_j(d.hidden)), one_lds(d));
+}
+
 hipError_t launch_moe_block_noalloc(const uint8_t* pool, const kq_moe_desc& d, const void* R,
                                     bool r_f32, const void* X, bool x_f32, uint32_t batch,
                                     uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H, void* Y,
@@ -1752,7 +2289,8 @@ hipError_t launch_moe_block_noalloc(const uint8_t* pool, const kq_moe_desc& d, c
     void* ws = nullptr;
     const hipError_t e = scratch_ptr(&ws, s);
     if (e != hipSuccess) return e;
-    return launch_moe_block(pool, d, R, r_f32, X, x_f32, batch, idx, wgt, xh, H, Y, y_f32, ws, s);
+    return launch_moe_block(pool, d, R, r_f32, X, x_f32, batch, idx, wgt, xh, H, Y, y_f32, ws, s,
+                            KQ_MOE_PATH_AUTO);
 }
 
 hipError_t launch_moe_logits(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
@@ -1789,7 +2327,8 @@ hipError_t launch_moe_down(const uint8_t* pool, const kq_moe_desc& d, const uint
     return launch_dn<false>(pool, d, idx, wgt, nullptr, H, Y, y_f32, batch, s);
 }
 
-// The block's three launches. With the streaming gate/up (1-2 tokens) the
+// The block: three launches (KQ_MOE_PATH_ONE: the one-launch kernel). With
+// the streaming gate/up (1-2 tokens) the
 // router's top-k tail moves into the gate/up launch: every gate/up workgroup
 // selects from the logits (cheap, L2-resident) instead of the router's last
 // workgroup doing it after a device-scope hand-off (measured 8.1 -> 3.3 us
@@ -1797,9 +2336,11 @@ hipError_t launch_moe_down(const uint8_t* pool, const kq_moe_desc& d, const uint
 hipError_t launch_moe_block(const uint8_t* pool, const kq_moe_desc& d, const void* R, bool r_f32,
                             const void* X, bool x_f32, uint32_t batch, uint32_t* idx, float* wgt,
                             uint16_t* xh, uint16_t* H, void* Y, bool y_f32, void* ws,
-                            hipStream_t s) {
+                            hipStream_t s, int path) {
     const WsLayout L = ws_layout(d, batch);
     uint8_t* w = reinterpret_cast<uint8_t*>(ws);
+    if (path == KQ_MOE_PATH_ONE)
+        return launch_one(pool, d, R, r_f32, X, x_f32, idx, wgt, xh, H, Y, y_f32, w, L, s);
     Plan* plan = reinterpret_cast<Plan*>(w + L.plan);
     const uint16_t* xin = x_f32 ? xh : reinterpret_cast<const uint16_t*>(X);
     hipError_t e;

@@ -18,6 +18,8 @@ LIB_PATH = os.path.join(HERE, "_lib", "libkq.so")
 KQ_OK, KQ_EINVAL, KQ_ENULL, KQ_EALIGN, KQ_EUNSUPPORTED, KQ_EWORKSPACE, KQ_EHIP = range(7)
 F16, BF16, F32 = 0, 1, 2
 PATH_AUTO, PATH_VALU, PATH_MFMA = 0, 1, 2
+MOE_PATH_AUTO, MOE_PATH_LAUNCHES, MOE_PATH_ONE = 0, 1, 2  # KQ_MOE_PATH_*
+MOE_WS_ERR_OFFSET = 128  # KQ_MOE_WS_ERR_OFFSET
 
 # every symbol include/kq.h declares
 EXPORTS = ("kq_status_str", "kq_last_hip_error", "kq_version", "kq_int4_gemv",
@@ -25,7 +27,7 @@ EXPORTS = ("kq_status_str", "kq_last_hip_error", "kq_version", "kq_int4_gemv",
            "kq_stream_read_cfg",
            "kq_vq_gemv", "kq_moe_default_desc", "kq_moe_workspace_size",
            "kq_moe_workspace_init", "kq_moe_router_topk", "kq_moe_gate_up_swiglu",
-           "kq_moe_down_combine", "kq_moe_block", "kq_moe_block_noalloc",
+           "kq_moe_down_combine", "kq_moe_block", "kq_moe_block_path", "kq_moe_block_noalloc",
            "kq_moe_unfused_workspace_size",
            "kq_moe_block_unfused", "kq_vq_quantize_workspace_size", "kq_vq_quantize")
 
@@ -86,6 +88,8 @@ def lib():
                                           sz, vp]
         L.kq_moe_block.argtypes = [vp, C.POINTER(MoEDesc), vp, i32, vp, i32, u32, vp, vp, vp, vp,
                                    vp, i32, vp, sz, vp]
+        L.kq_moe_block_path.argtypes = [vp, C.POINTER(MoEDesc), vp, i32, vp, i32, u32, vp, vp, vp,
+                                        vp, vp, i32, vp, sz, i32, vp]
         L.kq_moe_block_noalloc.argtypes = [vp, C.POINTER(MoEDesc), vp, i32, vp, i32, u32, vp, vp,
                                            vp, vp, vp, i32, vp]
         L.kq_moe_unfused_workspace_size.argtypes = [C.POINTER(MoEDesc)]
@@ -275,12 +279,20 @@ def moe_down_combine(pool, desc, idx, wgt, H, y, ws, ws_bytes, batch=1, stream=N
            "kq_moe_down_combine")
 
 
-def moe_block(pool, desc, R, x, idx, wgt, H, y, ws, ws_bytes, batch=1, xh=None, stream=None):
+def moe_block(pool, desc, R, x, idx, wgt, H, y, ws, ws_bytes, batch=1, xh=None, stream=None,
+              path=None):
     """encodeFused (moe-fused/src/main.mm:176-206): router_topk ->
-    gate_up_swiglu -> down_combine on one stream."""
-    _check(lib().kq_moe_block(_ptr(pool), C.byref(desc), _ptr(R), _dt(R), _ptr(x), _dt(x), batch,
-                              _ptr(idx), _ptr(wgt), _ptr(xh), _ptr(H), _ptr(y), _dt(y), _ptr(ws),
-                              ws_bytes, _stream(stream)), "kq_moe_block")
+    gate_up_swiglu -> down_combine on one stream. path (MOE_PATH_*): the
+    launch structure (None: kq_moe_block, the same as MOE_PATH_AUTO)."""
+    if path is None:
+        _check(lib().kq_moe_block(_ptr(pool), C.byref(desc), _ptr(R), _dt(R), _ptr(x), _dt(x),
+                                  batch, _ptr(idx), _ptr(wgt), _ptr(xh), _ptr(H), _ptr(y), _dt(y),
+                                  _ptr(ws), ws_bytes, _stream(stream)), "kq_moe_block")
+    else:
+        _check(lib().kq_moe_block_path(_ptr(pool), C.byref(desc), _ptr(R), _dt(R), _ptr(x),
+                                       _dt(x), batch, _ptr(idx), _ptr(wgt), _ptr(xh), _ptr(H),
+                                       _ptr(y), _dt(y), _ptr(ws), ws_bytes, path,
+                                       _stream(stream)), "kq_moe_block_path")
 
 
 MOE_NOALLOC_WS_BYTES = 1 << 20  # KQ_MOE_NOALLOC_WS_BYTES

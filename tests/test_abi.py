@@ -166,6 +166,21 @@ def test_moe_rejects_on_host():
     assert L.kq_moe_workspace_init(FAKE + 4, 64, None) == kq.KQ_EALIGN
 
 
+def test_moe_block_path_rejects_on_host():
+    """kq_moe_block_path: an unknown path is KQ_EINVAL, the one-launch path
+    outside its limits (here two tokens) KQ_EUNSUPPORTED, before any launch."""
+    L = kq.lib()
+    d = kq.moe_default_desc()
+    n = kq.moe_workspace_size(d, 2)
+
+    def call(batch, path):
+        return L.kq_moe_block_path(FAKE, C.byref(d), FAKE, kq.F16, FAKE, kq.F16, batch, FAKE, FAKE,
+                                   None, FAKE, FAKE, kq.F32, FAKE, n, path, None)
+    assert call(1, 3) == kq.KQ_EINVAL
+    assert call(1, -1) == kq.KQ_EINVAL
+    assert call(2, kq.MOE_PATH_ONE) == kq.KQ_EUNSUPPORTED
+
+
 def test_moe_unfused_rejects_on_host():
     L = kq.lib()
     d = kq.moe_default_desc()
