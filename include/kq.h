@@ -41,8 +41,17 @@ typedef enum kq_status {
 
 typedef enum kq_dtype { KQ_F16 = 0, KQ_BF16 = 1, KQ_F32 = 2 } kq_dtype;
 
-/* Kernel family used by kq_int4_gemv_path (0 picks by batch size). */
-typedef enum kq_int4_path { KQ_PATH_AUTO = 0, KQ_PATH_VALU = 1, KQ_PATH_MFMA = 2 } kq_int4_path;
+/* Kernel family used by kq_int4_gemv_path (0 picks by batch size).
+ * KQ_PATH_SCALAR: the debug scalar kernel, one thread per (row, token) with
+ * a plain per-chunk loop and no staging, after gemv_int4_scalar (v0,
+ * int4-gemv/src/kernels.metal:71-95) -- slow, for checking the fast paths
+ * on the device; AUTO never picks it. */
+typedef enum kq_int4_path {
+    KQ_PATH_AUTO = 0,
+    KQ_PATH_VALU = 1,
+    KQ_PATH_MFMA = 2,
+    KQ_PATH_SCALAR = 3
+} kq_int4_path;
 
 const char* kq_status_str(kq_status s);
 /* hipError_t of the last KQ_EHIP returned on this host thread (0 if none). */
@@ -77,8 +86,10 @@ kq_status kq_int4_gemv(const uint32_t* W, const void* S, const void* B, kq_dtype
                        uint32_t M, uint32_t K, uint32_t G, uint32_t batch,
                        kq_stream_t stream);
 
-/* kq_int4_gemv with the kernel family forced (VALU dot2 path or MFMA
- * 16x16x32 path); used to measure the crossover. Same contract. */
+/* kq_int4_gemv with the kernel family forced (VALU dot2 path, MFMA
+ * 16x16x32 path, or the debug scalar kernel); used to measure the crossover
+ * and to cross-check the paths. Same contract (the scalar kernel has no K
+ * limit beyond it). */
 kq_status kq_int4_gemv_path(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,
                             const uint16_t* X, void* Y, kq_dtype y_dtype,
                             uint32_t M, uint32_t K, uint32_t G, uint32_t batch,

@@ -18,7 +18,7 @@ LIB_DIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(LIB_DIR, "libkq.so")
 DRV_SRC = os.path.join(HERE, "drivers")
 BIN_DIR = os.path.join(HERE, "_bin")
-DRIVERS = ("int4gemv", "vqgemv", "moefused")
+DRIVERS = ("int4gemv", "vqgemv", "moefused", "moepipe")
 ARCH = "gfx950"
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 

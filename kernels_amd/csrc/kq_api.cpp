@@ -85,6 +85,8 @@ kq_status run_int4(const uint32_t* W, const void* S, const void* B, kq_dtype sb_
         if (!mfma_ok) return KQ_EUNSUPPORTED;
         return hip_status(kq::launch_int4_mfma(W, Sp, Bp, mk, inter, X, Y, yf, M, K, G, batch, mcfg, s));
     }
+    if (path == KQ_PATH_SCALAR)
+        return hip_status(kq::launch_int4_scalar(W, Sp, Bp, mk, inter, X, Y, yf, M, K, G, batch, s));
     return KQ_EINVAL;
 }
 
@@ -163,7 +165,9 @@ kq_status kq_int4_gemv(const uint32_t* W, const void* S, const void* B, kq_dtype
 kq_status kq_int4_gemv_path(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,
                             const uint16_t* X, void* Y, kq_dtype y_dtype, uint32_t M, uint32_t K,
                             uint32_t G, uint32_t batch, kq_int4_path path, kq_stream_t stream) {
-    if (!(path == KQ_PATH_AUTO || path == KQ_PATH_VALU || path == KQ_PATH_MFMA)) return KQ_EINVAL;
+    if (!(path == KQ_PATH_AUTO || path == KQ_PATH_VALU || path == KQ_PATH_MFMA ||
+          path == KQ_PATH_SCALAR))
+        return KQ_EINVAL;
     return run_int4(W, S, B, sb_dtype, X, Y, y_dtype, M, K, G, batch, path, nullptr, stream);
 }
 

@@ -510,6 +510,58 @@ hipError_t launch_int4_valu(const uint32_t* W, const uint16_t* S, const uint16_t
 }
 
 // ---------------------------------------------------------------------------
+// Debug scalar path (KQ_PATH_SCALAR), after gemv_int4_scalar (v0,
+// int4-gemv/src/kernels.metal:71-95): one thread per (row, token), the row
+// walked one 32-weight chunk at a time with plain loads -- d = sum q_k x_k
+// and xs = sum x_k of the chunk in fp32, then acc += s * d + b * xs. No
+// LDS, no shared staging, no rings: the device-side reference the fast
+// paths can be checked against. Slow by design (each thread streams its own
+// row).
+// ---------------------------------------------------------------------------
+template <int MK>
+__global__ __launch_bounds__(256) void int4_scalar_k(const uint32_t* __restrict__ W,
+                                                     const uint16_t* __restrict__ S,
+                                                     const uint16_t* __restrict__ B, int inter,
+                                                     const uint16_t* __restrict__ X, void* Y,
+                                                     int yf, uint32_t M, uint32_t K, uint32_t G) {
+    const uint32_t m = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
+    if (m >= M) return;
+    const uint32_t groups = K / G;
+    const uint32_t* w = W + (size_t)m * (K / 8);
+    const uint16_t* x = X + (size_t)t * K;
+    float acc = 0.0f;
+    for (uint32_t c = 0; c < K / 32; ++c) {
+        float d = 0.0f, xs = 0.0f;
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t p = w[c * 4 + i];
+            for (uint32_t n = 0; n < 8; ++n) {
+                const float xv = h2f(x[c * 32 + i * 8 + n]);
+                d = fmaf((float)((p >> (4 * n)) & 0xFu), xv, d);
+                xs += xv;
+            }
+        }
+        const size_t g = (size_t)m * groups + c * 32 / G;
+        const float sc = meta2f<MK>(inter ? S[2 * g] : S[g]);
+        const float bs = meta2f<MK>(inter ? S[2 * g + 1] : B[g]);
+        acc = fmaf(sc, d, fmaf(bs, xs, acc));
+    }
+    if (yf) reinterpret_cast<float*>(Y)[(size_t)t * M + m] = acc;
+    else reinterpret_cast<uint16_t*>(Y)[(size_t)t * M + m] = f2h(acc);
+}
+
+hipError_t launch_int4_scalar(const uint32_t* W, const uint16_t* S, const uint16_t* B,
+                              int meta_kind, bool interleaved, const uint16_t* X, void* Y,
+                              bool y_f32, uint32_t M, uint32_t K, uint32_t G, uint32_t batch,
+                              hipStream_t s) {
+    const dim3 grid((M + 255) / 256, batch);
+    if (meta_kind == 1)
+        int4_scalar_k<1><<<grid, 256, 0, s>>>(W, S, B, interleaved ? 1 : 0, X, Y, y_f32 ? 1 : 0, M, K, G);
+    else
+        int4_scalar_k<0><<<grid, 256, 0, s>>>(W, S, B, interleaved ? 1 : 0, X, Y, y_f32 ? 1 : 0, M, K, G);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // xsum32 (int4-gemv/src/kernels.metal:54-65): one thread per 32-chunk, the
 // chunk summed as eight half4 groups, each group left to right.
 // ---------------------------------------------------------------------------

@@ -39,6 +39,11 @@ Int4Cfg int4_mfma_default(uint32_t M, uint32_t K, uint32_t batch);
 // Tokens one matrix-core pass takes (all of them; 0: the shape is not supported).
 uint32_t int4_mfma_tokens_per_pass(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg);
 
+// Debug scalar path: one thread per (row, token), plain chunk loop (v0).
+hipError_t launch_int4_scalar(const uint32_t* W, const uint16_t* S, const uint16_t* B,
+                              int meta_kind, bool interleaved, const uint16_t* X, void* Y,
+                              bool y_f32, uint32_t M, uint32_t K, uint32_t G, uint32_t batch,
+                              hipStream_t s);
 hipError_t launch_xsum32(const uint16_t* X, float* xs, uint32_t K, uint32_t batch, hipStream_t s);
 // unroll 0 and threads 0: the default shape (U = 1, 2048 x 256 threads)
 hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, uint32_t unroll,

@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(HERE, "_lib", "libkq.so")
 
 KQ_OK, KQ_EINVAL, KQ_ENULL, KQ_EALIGN, KQ_EUNSUPPORTED, KQ_EWORKSPACE, KQ_EHIP = range(7)
 F16, BF16, F32 = 0, 1, 2
-PATH_AUTO, PATH_VALU, PATH_MFMA = 0, 1, 2
+PATH_AUTO, PATH_VALU, PATH_MFMA, PATH_SCALAR = 0, 1, 2, 3
 MOE_PATH_AUTO, MOE_PATH_LAUNCHES, MOE_PATH_ONE = 0, 1, 2  # KQ_MOE_PATH_*
 MOE_WS_ERR_OFFSET = 128  # KQ_MOE_WS_ERR_OFFSET
 

@@ -16,12 +16,13 @@ import numpy as np
 import pytest
 
 import oracle
+from kernels_amd import gen
 from tests._util import assert_close, inf_rel
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BIN = os.path.join(ROOT, "kernels_amd", "_bin")
 GOLD = os.path.join(os.path.dirname(__file__), "golden")
-DRIVERS = ("int4gemv", "vqgemv", "moefused")
+DRIVERS = ("int4gemv", "vqgemv", "moefused", "moepipe")
 
 
 def _exe(name):
@@ -137,3 +138,78 @@ def test_moefused_driver(tmp_path, batch):
     got = np.fromfile(tmp_path / "y.f32", np.float32).astype(np.float64).reshape(batch, -1)
     assert_close(got, Y, what="moefused y")
     assert inf_rel(got, Y) < 2e-3
+
+
+@pytest.mark.gpu
+def test_moefused_driver_store(tmp_path):
+    """The real-weight path: an expert store in the reference's on-disk
+    layout (n_experts blobs of 14,024,704 B, moe-fused/src/main.mm:129-149)
+    written from gen.moe_pool, read back by moefused --store with pread. The
+    dumped selected experts equal the store's bytes (the loader read the
+    right blobs), routing equals the oracle's on the reference's LCG inputs,
+    and y equals the oracle's block computed from the store. The reference's
+    own real-weight golden (moe-fused/results/y_metal.f32) needs its
+    experts.bin, which is not in this image: that output stays unpinned."""
+    n = 16
+    d = oracle.MoEDesc(2880, 2880, n, 4, 14024704, 0, 4671360, 9342720, 0, 4147200, 4406400,
+                       4665600)
+    host = gen.moe_pool(n, seed=4242, quantize=True)
+    store = tmp_path / "experts.bin"
+    host.tofile(store)
+    dump = tmp_path / "dump"
+    dump.mkdir()
+    out = _run("moefused", "--store", store, "--experts", n, "--batch", 1, "--resident", 1,
+               "--iters", 2, "--warmup", 1, "--repeat", 2, "--dump", dump)
+    assert "FAIL" not in out and "loading 16 experts" in out
+    rows = [l.split() for l in open(dump / "topk.txt").read().splitlines()]
+    idx = np.array([int(r[0]) for r in rows], np.uint32).reshape(1, -1)
+    wgt = np.array([float(r[1]) for r in rows]).reshape(1, -1)
+    R, X = _lcg_inputs(n, d.hidden, 1)
+    oidx, owgt, _ = oracle.moe_router(R, oracle.F32, X, oracle.F32, 1, d)
+    assert np.array_equal(oidx, idx)
+    np.testing.assert_allclose(wgt, owgt, atol=1e-6, rtol=0)
+    blobs = host.reshape(n, d.blob)
+    for e in idx.ravel().tolist():
+        assert np.array_equal(np.fromfile(dump / f"expert_{e}.bin", np.uint8), blobs[e]), e
+    Xh = X.astype(np.float16).view(np.uint16)
+    H = oracle.moe_gate_up(host, d, oidx, Xh, oracle.F16, 1)
+    Y = oracle.moe_down(host, d, oidx, owgt, H.astype(np.float16).view(np.uint16), 1)
+    got = np.fromfile(dump / "y.f32", np.float32).astype(np.float64).reshape(1, -1)
+    assert_close(got, Y, what="moefused --store y")
+    assert inf_rel(got, Y) < 2e-3
+
+
+@pytest.mark.gpu
+def test_moepipe_store(tmp_path):
+    """The expert streaming pipeline (moe-pipeline/src/main.mm): 12 experts
+    of a store file streamed through 5 pinned slots (depth 3) and 2 HBM
+    slots, every expert computed as it lands. The driver compares every
+    expert's y of the pipelined run with the stop-and-wait run bit for bit
+    (same kernels and inputs: a slot overwritten too early would show);
+    expert 0's h and y, dumped by --verify, are checked against the oracle."""
+    n = 12
+    blob = 14024704
+    host = gen.moe_pool(n, seed=777, quantize=False)
+    store = tmp_path / "experts.bin"
+    host.tofile(store)
+    vd = tmp_path / "verify"
+    vd.mkdir()
+    out = _run("moepipe", "--store", store, "--experts", n, "--depth", 3, "--workers", 2,
+               "--reps", 1, "--verify", vd)
+    assert f"pipe outputs == seq outputs (bitwise, {n} experts): OK" in out
+    off = int(open(vd / "meta.txt").read().split()[0])
+    assert off % blob == 0
+    e = off // blob
+    d = oracle.MoEDesc(2880, 2880, n, 1, blob, 0, 4671360, 9342720, 0, 4147200, 4406400, 4665600)
+    x = np.fromfile(vd / "x.f32", np.float32)
+    k = np.arange(2880)
+    assert np.array_equal(x, (np.float32(0.05) * ((k % 17) - 8)).astype(np.float32))
+    Xh = x.reshape(1, -1).astype(np.float16).view(np.uint16)
+    idx = np.array([[e]], np.uint32)
+    H = oracle.moe_gate_up(host, d, idx, Xh, oracle.F16, 1)
+    h = np.fromfile(vd / "h.f16", np.float16).astype(np.float64).reshape(H.shape)
+    assert_close(h, H, what="moepipe h")
+    Y = oracle.moe_down(host, d, idx, np.ones((1, 1)), h.astype(np.float16).view(np.uint16), 1)
+    y = np.fromfile(vd / "y.f32", np.float32).astype(np.float64).reshape(1, -1)
+    assert_close(y, Y, what="moepipe y")
+    assert inf_rel(y, Y) < 2e-3

@@ -159,3 +159,26 @@ def test_mfma_forced_plan_unsupported(gpu):
     with pytest.raises(kq.KQError) as e:
         run_int4(p, gpu, path=kq.PATH_MFMA, rows=4, unroll=13)  # ring depth is 2
     assert e.value.status == kq.KQ_EUNSUPPORTED
+
+
+@pytest.mark.parametrize("layout,sb", [("sb", kq.F16), ("split", kq.F16), ("split", kq.BF16)])
+@pytest.mark.parametrize("M,K,G,batch", [(777, 4096, 64, 1), (129, 2880, 32, 3), (64, 32768, 128, 2),
+                                         (4096, 14336, 64, 1)])
+def test_scalar_debug_path(gpu, layout, sb, M, K, G, batch):
+    """The debug scalar kernel (v0's one-thread-per-row loop) against the
+    oracle, and the vector path against it (K = 32768: past the vector
+    path's LDS bound, which only the scalar kernel takes)."""
+    p = gen.int4_problem(M, K, G, batch=batch, seed=M + K + G)
+    if sb == kq.BF16:
+        rng = np.random.default_rng(M)
+        S = gen.bf16_bits(np.abs(rng.normal(0, 0.02, (M, K // G))))
+        B = gen.bf16_bits(rng.normal(0, 0.02, (M, K // G)))
+        ref = oracle.int4_gemv(p["W"], S, B, p["X"], M, K, G, 0, oracle.BF16)
+        got = run_int4(p, gpu, layout="split", sb_dtype=kq.BF16, S=S, B=B, path=kq.PATH_SCALAR)
+    else:
+        ref = ref_int4(p, layout)
+        got = run_int4(p, gpu, layout=layout, path=kq.PATH_SCALAR)
+    check(got, ref, f"scalar {layout} {M}x{K} G{G} b{batch}")
+    if K <= 29120 and sb == kq.F16:
+        fast = run_int4(p, gpu, layout=layout, path=kq.PATH_VALU)
+        assert_close(fast, got, what="vector path vs scalar")
