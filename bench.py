@@ -468,15 +468,19 @@ def bench_vq(torch, kq, dev, args, timer, res):
 
 
 def bench_skinny(torch, kq, dev, args, timer, res):
+    """Both config-2 shapes at each of --skinny-batches tokens through the
+    vector path, the matrix cores and AUTO's choice, each a HIP graph over 8
+    weight copies (940 MB per shape, so every byte comes from HBM)."""
     out = {}
     ncopy = 8
+    batches = [int(b) for b in args.skinny_batches.split(",")]
     for M, K in ((28672, 8192), (8192, 28672)):
         layers = make_int4_layers(torch, dev, ncopy, [("w", M, K)], seed=M)
-        for batch in (1, 2, 4, 8, 16):
+        for batch in batches:
             x = torch.randn((batch, K), device=dev).half()
             y = torch.empty((batch, M), dtype=torch.float16, device=dev)
             row = {}
-            for pname, path in (("valu", kq.PATH_VALU), ("mfma", kq.PATH_MFMA)):
+            for pname, path in (("valu", kq.PATH_VALU), ("mfma", kq.PATH_MFMA), ("auto", kq.PATH_AUTO)):
                 def one(path=path):
                     for L in layers:
                         W, SB, _, _ = L["w"]
@@ -592,6 +596,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--sections", default="step,ceiling,roofline,moe,vq,skinny,cpu")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--skinny-batches", default="1,2,3,4,8,16")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "

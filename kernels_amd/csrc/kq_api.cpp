@@ -63,9 +63,11 @@ kq_status run_int4(const uint32_t* W, const void* S, const void* B, kq_dtype sb_
     // 4- or 8-byte word each
     const bool meta_aligned = inter || (aligned(S, 8) && aligned(B, 8));
     const bool mfma_ok = meta_aligned && kq::int4_mfma_supported(M, K, G, batch, mcfg);
-    // Crossover: a vector pass takes 2 tokens, the matrix-core pass all of
-    // them; one matrix-core pass costs ~1.7 vector passes (64-byte row pieces
-    // per load instead of 1 KiB rows). Take the fewer W reads.
+    // Crossover, in batch-1 vector passes: a vector pass takes up to 4 tokens
+    // (int4_valu_cost), a matrix-core pass all of them at ~1.2 (29.3-30.3 us
+    // against 24.9 us at 28672 x 8192; 64-byte row pieces per load instead of
+    // 1 KiB rows). Measured: the vector path wins at 1-2 tokens, the matrix
+    // cores from 3.
     if (path == KQ_PATH_AUTO) {
         if (!mfma_ok) {
             path = KQ_PATH_VALU;
@@ -73,8 +75,8 @@ kq_status run_int4(const uint32_t* W, const void* S, const void* B, kq_dtype sb_
             path = KQ_PATH_MFMA;
         } else {
             const uint32_t tpp = kq::int4_mfma_tokens_per_pass(M, K, G, batch, mcfg);
-            const uint32_t mp = tpp ? (batch + tpp - 1) / tpp : 1000, vp = (batch + 1) / 2;
-            path = 17 * mp < 10 * vp ? KQ_PATH_MFMA : KQ_PATH_VALU;
+            const uint32_t mp = tpp ? (batch + tpp - 1) / tpp : 1000;
+            path = 120 * mp < kq::int4_valu_cost(M, K, batch) ? KQ_PATH_MFMA : KQ_PATH_VALU;
         }
     }
     if (path == KQ_PATH_VALU) {

@@ -99,10 +99,11 @@ __host__ __device__ inline size_t vlds_x(uint32_t ntok, uint32_t nchp) {
 constexpr uint32_t kXBlk = 4608;
 constexpr int kXr = 8;  // x words a thread stages per pass (one pass up to 8 x threads)
 
-// Register budget: a ring of R * D >= 16 row-steps needs more than 128
-// VGPRs, so those instantiations run at most 8 waves per workgroup.
+// Register budget: a ring of R * D >= 16 row-steps, or 3-4 tokens per pass,
+// needs more than 128 VGPRs, so those instantiations run at most 8 waves per
+// workgroup.
 template <int NB, int R, int D, bool SB, bool BF, bool GA>
-__global__ __launch_bounds__(R * D >= 16 ? 512 : 1024) void int4_valu(VArgs A) {
+__global__ __launch_bounds__(R * D >= 16 || NB >= 3 ? 512 : 1024) void int4_valu(VArgs A) {
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr uint32_t MB = SB ? 4 : 2;  // metadata bytes per group and array
     constexpr uint32_t kOOB = 0x80000000u;  // past every descriptor's range: loads read zeros
@@ -341,7 +342,10 @@ __global__ __launch_bounds__(R * D >= 16 ? 512 : 1024) void int4_valu(VArgs A) {
 
 
 constexpr size_t kLdsMax = 160 * 1024;
-constexpr uint32_t kMaxNB = 2;  // tokens per pass of the vector path
+// Tokens per pass of the vector path: up to 4 (x of every token of the pass
+// in LDS, NB accumulators per row); a batch takes passes of 4, then 3, 2 or
+// 1, each reading W once. A pass whose x does not fit LDS takes 2 tokens.
+constexpr uint32_t kMaxNB = 4;
 
 uint32_t log2u(uint32_t v) {
     uint32_t r = 0;
@@ -376,7 +380,9 @@ bool make_vplan(uint32_t M, uint32_t K, uint32_t ntok, Int4Cfg cfg, VPlan& out) 
             // waves with a ring of up to 16 items
             for (uint32_t wcap = kMaxWaves; wcap >= 8; wcap /= 2) {
                 if (P > wcap) continue;
-                const uint32_t dmax = wcap > 8 ? 8 / R : (ntok == 2 && R == 2 ? 8 : 16);
+                if (ntok >= 3 && wcap > 8) continue;  // 8 waves at 3-4 tokens (registers)
+                uint32_t dmax = wcap > 8 ? 8 / R : (ntok == 2 && R == 2 ? 8 : 16);
+                if (ntok >= 3) dmax = dmax < 4 ? dmax : 4;  // 3-4 tokens: rings of 2 or 4
                 if (cfg.unroll > 0 && (uint32_t)cfg.unroll > dmax) continue;
                 const uint32_t qmax = wcap / P;
                 const uint32_t rounds = (per_cu + qmax - 1) / qmax;
@@ -427,9 +433,12 @@ hipError_t vgo_d(const VArgs& a, const VPlan& pl, hipStream_t s) {
     switch (pl.D) {
         case 2: return vgo<NB, R, 2, SB, BF, GA>(a, pl, s);
         case 4: return vgo<NB, R, 4, SB, BF, GA>(a, pl, s);
-        case 8: return vgo<NB, R, 8, SB, BF, GA>(a, pl, s);
+        case 8:
+            if constexpr (NB >= 3) return hipErrorInvalidValue;  // plans give 3-4 tokens D <= 4
+            else return vgo<NB, R, 8, SB, BF, GA>(a, pl, s);
         case 16:  // two tokens on two rows: a 16-deep ring would spill
-            if constexpr (NB == 2 && R == 2) return hipErrorInvalidValue;
+            if constexpr (NB >= 2 && R == 2) return hipErrorInvalidValue;
+            else if constexpr (NB >= 3) return hipErrorInvalidValue;
             else return vgo<NB, R, 16, SB, BF, GA>(a, pl, s);
         default: return hipErrorInvalidValue;
     }
@@ -450,6 +459,23 @@ hipError_t vgo_nb(const VArgs& a, const VPlan& pl, bool sb, bool bf, hipStream_t
 
 Int4Cfg int4_valu_default(uint32_t, uint32_t, uint32_t) { return Int4Cfg{0, 0}; }
 
+// Cost of `batch` tokens on the vector path in batch-1 passes: passes of 4,
+// then 3, 2 or 1 tokens (fewer where x does not fit LDS), a pass of n tokens
+// costing 1, 1.12, 1.37, 1.58 (x100) batch-1 passes -- measured at 28672 x
+// 8192 and 8192 x 28672 (24.9, 27.9, 34.1, 39.4 us at 1-4 tokens).
+uint32_t int4_valu_cost(uint32_t M, uint32_t K, uint32_t batch) {
+    static constexpr uint32_t kPass[5] = {0, 100, 112, 137, 158};
+    uint32_t cost = 0;
+    for (uint32_t t0 = 0; t0 < batch;) {
+        uint32_t nb = batch - t0 >= kMaxNB ? kMaxNB : batch - t0;
+        VPlan pl;
+        while (nb > 1 && !make_vplan(M, K, nb, Int4Cfg{0, 0}, pl)) nb = nb > 2 ? 2 : 1;
+        cost += kPass[nb];
+        t0 += nb;
+    }
+    return cost;
+}
+
 size_t int4_valu_lds_bytes(uint32_t K, uint32_t batch) {
     const uint32_t nchp = ((K >> 5) + 63) / 64 * 64;
     return vlds_x(batch < kMaxNB ? batch : kMaxNB, nchp);
@@ -469,11 +495,11 @@ hipError_t launch_int4_valu(const uint32_t* W, const uint16_t* S, const uint16_t
     // the gathered form is built for the MoE expert layout: one token, split bf16 S and B
     if (gsel != nullptr && (batch != 1 || interleaved || meta_kind != 1)) return hipErrorInvalidValue;
     for (uint32_t t0 = 0; t0 < batch;) {
-        uint32_t nb = batch - t0 >= kMaxNB ? kMaxNB : 1;
+        uint32_t nb = batch - t0 >= kMaxNB ? kMaxNB : batch - t0;
         VPlan pl;
-        if (!make_vplan(M, K, nb, cfg, pl)) {
-            if (nb == 1 || !make_vplan(M, K, 1, cfg, pl)) return hipErrorInvalidValue;
-            nb = 1;
+        while (!make_vplan(M, K, nb, cfg, pl)) {  // x of nb tokens too large for LDS
+            if (nb == 1) return hipErrorInvalidValue;
+            nb = nb > 2 ? 2 : 1;
         }
         VArgs a;
         a.W = W;
@@ -501,6 +527,8 @@ hipError_t launch_int4_valu(const uint32_t* W, const uint16_t* S, const uint16_t
         a.gstride = gstride;
         const bool bf = meta_kind == 1;
         const hipError_t e = gsel != nullptr ? vgo_r<1, false, true, true>(a, pl, s)
+                             : nb == 4       ? vgo_nb<4>(a, pl, interleaved, bf, s)
+                             : nb == 3       ? vgo_nb<3>(a, pl, interleaved, bf, s)
                              : nb == 2       ? vgo_nb<2>(a, pl, interleaved, bf, s)
                                              : vgo_nb<1>(a, pl, interleaved, bf, s);
         if (e != hipSuccess) return e;

@@ -20,6 +20,8 @@ uint32_t cu_count();
 // Default launch shape for a problem (tuning table).
 Int4Cfg int4_valu_default(uint32_t M, uint32_t K, uint32_t batch);
 size_t int4_valu_lds_bytes(uint32_t K, uint32_t batch);
+// `batch` tokens on the vector path in batch-1-pass units x 100 (AUTO's crossover).
+uint32_t int4_valu_cost(uint32_t M, uint32_t K, uint32_t batch);
 
 // gsel (device pointer, may be null): the kernel reads the matrix index
 // gsel[0] and moves W, S and B by gsel[0] * gstride bytes -- one matrix of a

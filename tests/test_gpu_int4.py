@@ -111,18 +111,20 @@ VALU_PLANS = [(8192, 1, 2), (8192, 1, 8), (8192, 2, 4), (8192, 4, 2), (8192, 4, 
 
 
 @pytest.mark.parametrize("K,parts,depth", VALU_PLANS)
-@pytest.mark.parametrize("M,batch", [(1031, 1), (70, 2)])
+@pytest.mark.parametrize("M,batch", [(1031, 1), (70, 2), (257, 4)])
 def test_forced_launch_shapes_agree(gpu, K, parts, depth, M, batch):
     """Every (K parts, ring depth) plan of the vector path gives the oracle's
     answer: split-K with the LDS reduction, padding items, a partial last
-    step (zero-padded x) and idle row lanes included."""
+    step (zero-padded x) and idle row lanes included. At 4 tokens a ring
+    deeper than 4 takes passes of fewer tokens."""
     p = gen.int4_problem(M, K, 64, batch=batch, seed=11 + K + parts)
     got = run_int4(p, gpu, path=kq.PATH_VALU, rows=parts, unroll=depth)
     check(got, ref_int4(p), f"P={parts} D={depth} K={K} M={M} b={batch}")
 
 
 @pytest.mark.parametrize("parts,depth,batch", [(2, 2, 1), (2, 4, 2), (4, 2, 1), (1, 16, 1),
-                                               (2, 16, 1), (1, 8, 2)])
+                                               (2, 16, 1), (1, 8, 2), (2, 2, 3), (2, 4, 4),
+                                               (4, 2, 4), (1, 4, 3), (4, 4, 7)])
 def test_forced_kparts_many_rounds(gpu, parts, depth, batch):
     """K parts over several rounds of row groups per workgroup: every
     round's partial sums wait in LDS until the one reduction at the end."""

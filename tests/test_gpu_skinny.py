@@ -1,6 +1,6 @@
 """Config 2: the batched skinny int4 GEMM at its own shapes, W 28672 x 8192
 (70B-class FFN up) and 8192 x 28672 (down), group 64, X fp16 [B][K] ~ N(0, 1),
-for B in {1, 2, 4, 8, 16}, on the vector path, the matrix-core path and AUTO,
+for B in {1, 2, 3, 4, 8, 16}, on the vector path, the matrix-core path and AUTO,
 each against the fp64 oracle through the C ABI.
 
 The batch-B oracle is the batch-1 oracle applied per row of X (no reference
@@ -21,7 +21,7 @@ from tests._util import assert_close, dev, inf_rel, to_f64
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(28672, 8192), (8192, 28672)]
-BATCHES = [1, 2, 4, 8, 16]
+BATCHES = [1, 2, 3, 4, 8, 16]
 PATHS = {"valu": kq.PATH_VALU, "mfma": kq.PATH_MFMA, "auto": kq.PATH_AUTO}
 
 
