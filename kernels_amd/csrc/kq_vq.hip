@@ -12,7 +12,8 @@
 //     64 lanes' 16-byte pieces of word jw in plane jw (conflict-free
 //     ds_read_b128 at immediate offsets; chunks past K zero-filled), and the
 //     codebook blocks of its rows (256 x half2 = 1 KiB each);
-//   * each index byte addresses one half2 codeword in LDS (ds_read_b32),
+//   * each index byte addresses one half2 codeword in LDS (ds_read_b32; one
+//     of 64 interleaved copies per lane, the address one v_perm_b32),
 //     dotted with its x pair by v_dot2_f32_f16 (fp32 accumulation); the
 //     lookups are shared by every token of the pass; the scale applies once
 //     per 32-weight chunk (scale_group % 32 == 0) or once per row;
@@ -56,10 +57,12 @@ struct QPlan {
 };
 
 // A lookup reads a random codebook entry per lane: with one copy, 64 random
-// indices meet in the 32 LDS banks (measured ~4 extra cycles per lookup).
-// kCbCopies interleaved copies (dword e * 32 + lane % 32) put every lane of a
-// half-wave in its own bank, at 32 KiB per codebook block.
-constexpr uint32_t kCbCopies = 32;
+// indices meet in the LDS banks (measured ~4 extra cycles per lookup).
+// kCbCopies interleaved copies (dword e * 64 + lane) put every lane in its own
+// bank, at 64 KiB per codebook block; the 256-byte entry stride makes a
+// lookup's address one byte permute of the index word (vq_word_perm: 2 VALU a
+// lookup instead of 3; 32 copies at a 128-byte stride took a shift and an add).
+constexpr uint32_t kCbCopies = 64;
 
 template <int R>
 struct QSlot {
@@ -90,6 +93,21 @@ __device__ __forceinline__ float vq_word(uint32_t word, u32x4 xv, const uint32_t
     acc = dot2(cbr[((word >> 16) & 0xFF) * CR], xv.z, acc);
     return dot2(cbr[(word >> 24) * CR], xv.w, acc);
 }
+// The same with kCbCopies = 64 copies at LDS offset 0: entry e of block b,
+// copy c at byte (b << 16) | (e << 8) | (c << 2), so one v_perm_b32 builds a
+// lookup's address from the index byte and cbase = (b << 16) | (lane << 2)
+// (byte 0 and 2 from cbase, byte 1 the index byte k of the word).
+// The kernel declares no static LDS, so its dynamic area starts at LDS
+// address 0 (the launcher checks that) and the address needs no base added.
+__device__ __forceinline__ uint32_t lds_u32(uint32_t addr) {
+    return *(const __attribute__((address_space(3))) uint32_t*)addr;
+}
+__device__ __forceinline__ float vq_word_perm(uint32_t word, u32x4 xv, uint32_t cbase, float acc) {
+    acc = dot2(lds_u32(__builtin_amdgcn_perm(word, cbase, 0x0C020400u)), xv.x, acc);
+    acc = dot2(lds_u32(__builtin_amdgcn_perm(word, cbase, 0x0C020500u)), xv.y, acc);
+    acc = dot2(lds_u32(__builtin_amdgcn_perm(word, cbase, 0x0C020600u)), xv.z, acc);
+    return dot2(lds_u32(__builtin_amdgcn_perm(word, cbase, 0x0C020700u)), xv.w, acc);
+}
 
 // x in LDS: per (step s, token t) one 4096-byte block of four planes (plane
 // jw = word jw of each of the 64 lanes' chunks, 16 B per lane) at
@@ -103,8 +121,10 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr uint32_t kOOB = 0x80000000u;  // past every descriptor's range: loads read zeros
     const uint32_t nch = A.nch, nchp = A.nchp, nw = A.K >> 3, nstep = nchp >> 6;
-    uint32_t* cb = reinterpret_cast<uint32_t*>(smem + qlds_x(NB, nchp));  // [ncb][256][CR]
-    float* part = reinterpret_cast<float*>(cb + (size_t)A.cb_first_div * 256 * CR);  // [rounds][waves][R*NB]
+    // LDS: the codebook blocks [ncb][256][CR] at offset 0, x, the K-part sums
+    uint32_t* cb = reinterpret_cast<uint32_t*>(smem);
+    unsigned char* xs = smem + (size_t)A.cb_first_div * 256 * CR * 4;
+    float* part = reinterpret_cast<float*>(xs + qlds_x(NB, nchp));  // [rounds][waves][R*NB]
 
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
     const uint32_t lane = tid & 63;
@@ -132,10 +152,14 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
             sv[r] = __builtin_amdgcn_raw_buffer_load_b128(rX, w < xtotal ? w * 16 : kOOB, 0, 0);
         }
     }
-    // codebook blocks of this workgroup's rows; with CR copies, item i is
-    // entry i / (CR / 4) and stores 4 of its copies
-    const uint32_t ncb_total = (A.M + A.rpc - 1) / A.rpc;
-    const uint32_t ncb = min(A.cb_first_div, ncb_total - cb0), cbn = ncb * 256;
+    // codebook blocks of this workgroup's rows (only those: the LDS area has
+    // room for cb_first_div, the most any workgroup's rows can touch); with
+    // CR copies, item i is entry i / (CR / 4) and stores 4 of its copies
+    const uint32_t row_last = row0 + rows_wg - 1;
+    const uint32_t cb_last = A.rpc_shift == 31 ? 0u
+                             : A.rpc_shift < 31 ? row_last >> A.rpc_shift
+                                                : row_last / A.rpc;
+    const uint32_t ncb = min(A.cb_first_div, cb_last - cb0 + 1), cbn = ncb * 256;
     const uint32_t* Cw = reinterpret_cast<const uint32_t*>(A.C) + (size_t)cb0 * 256;
     constexpr uint32_t kQd = CR == 1 ? 1 : CR / 4;  // items per entry
     constexpr int kCbPre = CR == 1 ? 4 : 8;          // items a thread preloads
@@ -191,7 +215,7 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
             const uint32_t w = r * nthr + tid;
             if (w < xtotal) {
                 const uint32_t t = w / nw, wi = w - t * nw, ch = wi >> 2;
-                *reinterpret_cast<u32x4*>(smem + ((ch >> 6) * NB + t) * kQBlk + (wi & 3) * 1024 +
+                *reinterpret_cast<u32x4*>(xs + ((ch >> 6) * NB + t) * kQBlk + (wi & 3) * 1024 +
                                           (ch & 63) * 16) = sv[r];
             }
         }
@@ -200,7 +224,7 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
         const uint32_t w = w0 + tid;
         if (w < xtotal) {
             const uint32_t t = w / nw, wi = w - t * nw, ch = wi >> 2;
-            *reinterpret_cast<u32x4*>(smem + ((ch >> 6) * NB + t) * kQBlk + (wi & 3) * 1024 +
+            *reinterpret_cast<u32x4*>(xs + ((ch >> 6) * NB + t) * kQBlk + (wi & 3) * 1024 +
                                       (ch & 63) * 16) = reinterpret_cast<const u32x4*>(A.X)[w];
         }
     }
@@ -208,7 +232,7 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
     for (uint32_t i = tid; i < NB * 4 * npad; i += nthr) {
         const uint32_t t = i / (4 * npad), rem = i - t * 4 * npad, jw = rem / npad;
         const uint32_t ch = nch + (rem - jw * npad);
-        *reinterpret_cast<u32x4*>(smem + ((ch >> 6) * NB + t) * kQBlk + jw * 1024 + (ch & 63) * 16) =
+        *reinterpret_cast<u32x4*>(xs + ((ch >> 6) * NB + t) * kQBlk + jw * 1024 + (ch & 63) * 16) =
             u32x4{0, 0, 0, 0};
     }
     auto cb_store = [&](uint32_t i, uint32_t v) __attribute__((always_inline)) {
@@ -266,7 +290,7 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
     const uint32_t rshift = A.rpc_shift;  // 31: every row uses the first block
     auto step = [&](const QSlot<R>& e, Cursor c, uint32_t n) __attribute__((always_inline)) {
         if (n >= A.nreal) return;  // padding to the ring depth (uniform)
-        const unsigned char* bx = smem + lane * 16 + (p * A.J + c.j) * (NB * kQBlk);
+        const unsigned char* bx = xs + lane * 16 + (p * A.J + c.j) * (NB * kQBlk);
         const uint32_t grp = min(g0 + c.round * A.Q + q, last_group);
         u32x4 xv[NB][4];
 #pragma unroll
@@ -282,13 +306,22 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
             uint32_t sr = e.sc[r];
             asm volatile("" : "+v"(iv), "+v"(sr));  // use the loaded values here, not earlier
             const float sc = h2f((uint16_t)sr);
-            const uint32_t* cbr = cb + blk * 256 * CR + (CR == 1 ? 0u : (lane & (CR - 1)));
 #pragma unroll
             for (int t = 0; t < NB; ++t) {
-                float da = vq_word<CR>(iv.x, xv[t][0], cbr, 0.0f);
-                float db = vq_word<CR>(iv.y, xv[t][1], cbr, 0.0f);
-                da = vq_word<CR>(iv.z, xv[t][2], cbr, da);
-                db = vq_word<CR>(iv.w, xv[t][3], cbr, db);
+                float da, db;
+                if constexpr (CR == 64) {
+                    const uint32_t cbase = (blk << 16) | (lane << 2);
+                    da = vq_word_perm(iv.x, xv[t][0], cbase, 0.0f);
+                    db = vq_word_perm(iv.y, xv[t][1], cbase, 0.0f);
+                    da = vq_word_perm(iv.z, xv[t][2], cbase, da);
+                    db = vq_word_perm(iv.w, xv[t][3], cbase, db);
+                } else {
+                    const uint32_t* cbr = cb + blk * 256 * CR + (CR == 1 ? 0u : (lane & (CR - 1)));
+                    da = vq_word<CR>(iv.x, xv[t][0], cbr, 0.0f);
+                    db = vq_word<CR>(iv.y, xv[t][1], cbr, 0.0f);
+                    da = vq_word<CR>(iv.z, xv[t][2], cbr, da);
+                    db = vq_word<CR>(iv.w, xv[t][3], cbr, db);
+                }
                 acc[r][t] = fmaf(sc, da + db, acc[r][t]);
             }
         }
@@ -392,10 +425,24 @@ hipError_t qgo(const QArgs& a, const QPlan& pl, hipStream_t s) {
     return hipGetLastError();
 }
 
+// The kCbCopies kernels address their codebooks from LDS address 0 (the
+// start of the dynamic area only while the kernel has no static LDS): checked
+// once per instantiation, with the one-copy kernel (same math, any LDS
+// layout) in its place otherwise.
+template <int NB, int R>
+hipError_t qgo_copies(const QArgs& a, const QPlan& pl, hipStream_t s) {
+    static const bool from_zero = [] {
+        hipFuncAttributes at{};
+        return hipFuncGetAttributes(&at, reinterpret_cast<const void*>(vq_valu<NB, R, 2, kCbCopies>)) ==
+                   hipSuccess &&
+               at.sharedSizeBytes == 0;
+    }();
+    return from_zero ? qgo<NB, R, kCbCopies>(a, pl, s) : qgo<NB, R, 1>(a, pl, s);
+}
+
 template <int NB>
 hipError_t qgo_nb(const QArgs& a, const QPlan& pl, hipStream_t s) {
-    if (pl.cr == kCbCopies)
-        return pl.R == 2 ? qgo<NB, 2, kCbCopies>(a, pl, s) : qgo<NB, 1, kCbCopies>(a, pl, s);
+    if (pl.cr == kCbCopies) return pl.R == 2 ? qgo_copies<NB, 2>(a, pl, s) : qgo_copies<NB, 1>(a, pl, s);
     return pl.R == 2 ? qgo<NB, 2, 1>(a, pl, s) : qgo<NB, 1, 1>(a, pl, s);
 }
 
