@@ -161,14 +161,28 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
                                                 : row_last / A.rpc;
     const uint32_t ncb = min(A.cb_first_div, cb_last - cb0 + 1), cbn = ncb * 256;
     const uint32_t* Cw = reinterpret_cast<const uint32_t*>(A.C) + (size_t)cb0 * 256;
-    constexpr uint32_t kQd = CR == 1 ? 1 : CR / 4;  // items per entry
-    constexpr int kCbPre = CR == 1 ? 4 : 8;          // items a thread preloads
-    const uint32_t cb_items = cbn * kQd;
+    // One copy: item i is entry i, a thread preloads kCbPre of them. With
+    // kCbCopies (at most 2 blocks fit in LDS): every wave loads each block
+    // with one 16-byte load per lane (lane l: entries 4l .. 4l + 3; the
+    // second block out of range when there is one), and stores copy groups
+    // of them below -- 1-2 load instructions a wave instead of the 8 that
+    // 4-byte loads of (entry, copy group) items took, which delayed the
+    // later waves' ring loads.
+    constexpr int kCbPre = 4;
+    const uint32_t cb_items = CR == 1 ? cbn : 0u;
     uint32_t cbv[kCbPre];
+    u32x4 cbq[2];
+    if constexpr (CR == 1) {
 #pragma unroll
-    for (int r = 0; r < kCbPre; ++r) {
-        const uint32_t i = r * nthr + tid;
-        cbv[r] = Cw[i < cb_items ? i / kQd : cbn - 1];
+        for (int r = 0; r < kCbPre; ++r) {
+            const uint32_t i = r * nthr + tid;
+            cbv[r] = Cw[i < cb_items ? i : cbn - 1];
+        }
+    } else {
+        const rsrc_t rC = make_rsrc(Cw, ncb * 1024);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+            cbq[b] = __builtin_amdgcn_raw_buffer_load_b128(rC, lane * 16 + (b < (int)ncb ? b * 1024u : kOOB), 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -235,18 +249,34 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
         *reinterpret_cast<u32x4*>(xs + ((ch >> 6) * NB + t) * kQBlk + jw * 1024 + (ch & 63) * 16) =
             u32x4{0, 0, 0, 0};
     }
-    auto cb_store = [&](uint32_t i, uint32_t v) __attribute__((always_inline)) {
-        if constexpr (CR == 1)
-            cb[i] = v;
-        else
-            *reinterpret_cast<u32x4*>(cb + (i / kQd) * CR + (i % kQd) * 4) = u32x4{v, v, v, v};
-    };
+    if constexpr (CR == 1) {
 #pragma unroll
-    for (int r = 0; r < kCbPre; ++r) {
-        const uint32_t i = r * nthr + tid;
-        if (i < cb_items) cb_store(i, cbv[r]);
+        for (int r = 0; r < kCbPre; ++r) {
+            const uint32_t i = r * nthr + tid;
+            if (i < cb_items) cb[i] = cbv[r];
+        }
+        for (uint32_t i = kCbPre * nthr + tid; i < cb_items; i += nthr) cb[i] = Cw[i];
+    } else {
+        // copy group g = copies 4g .. 4g + 3 of an entry (16 groups). Wave w
+        // stores groups (w' + l) % 16 of the lane's 4 entries for w' = w, w +
+        // waves, ... < 16: an entry's 64 copies span the 64 banks, so the 16
+        // lanes of a quarter-wave write 16 different groups (no conflicts),
+        // and over w' every (entry, group) is written once.
+        static_assert(CR == 64, "copy-group stores assume 64 copies");
+        const uint32_t nwv = nthr >> 6;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if (b >= (int)ncb) break;  // uniform
+            const uint32_t ev[4] = {cbq[b].x, cbq[b].y, cbq[b].z, cbq[b].w};
+            uint32_t* eb = cb + ((uint32_t)b * 256 + lane * 4) * CR;  // the lane's first entry
+            for (uint32_t w2 = wave; w2 < 16; w2 += nwv) {  // uniform
+                const uint32_t g = (w2 + lane) & 15;
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    *reinterpret_cast<u32x4*>(eb + k * CR + g * 4) = u32x4{ev[k], ev[k], ev[k], ev[k]};
+            }
+        }
     }
-    for (uint32_t i = kCbPre * nthr + tid; i < cb_items; i += nthr) cb_store(i, Cw[i / kQd]);
     __syncthreads();
 
     float acc[R][NB];
