@@ -1146,10 +1146,12 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
 // wave prefix sum gives every C_u, a ballot finds b's entry, and its expert
 // and slot masks come back by readlane.
 // Costs measured at 8 tokens: a row of a two-slot expert took 1.45x the
-// time of a one-slot row. Ring depth 4 (long per-wave streams here, ~40
-// items): 8 / 16 tokens 99.8 / 179.5 -> 98.8 / 170.9 us per block.
+// time of a one-slot row. Ring depth 3 (long per-wave streams here, ~40
+// items): against depth 4, 4 / 8 / 16 tokens 53.9 / 92.8 / 166.0 ->
+// 52.2 / 89.4 / 163.1 us per block (depth 4 held the one-slot gate/up at
+// 256 VGPRs with 3 spilled; depth 2: 51.3 / 89.9 / 166.1).
 constexpr uint32_t kPartRow = 4, kPartSlot = 3;
-constexpr int kPartD = 4;
+constexpr int kPartD = 3;
 struct PartAssign {
     uint32_t u, r0, nr, ex;  // u = 0xFFFFFFFF: no work for this workgroup
     uint64_t m0, m1;
