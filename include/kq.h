@@ -283,10 +283,22 @@ kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d,
  * inter need the same number of 1024-element steps, and each wave's down
  * rows fit its registers (ceil(ceil(hidden / (2 x CUs)) / floor(8 / top_k))
  * <= 4, 2 when hidden > 3072). New: the reference always encodes three
- * passes. */
+ * passes.
+ * KQ_MOE_PATH_ATOMIC: the reference's atomic sum(h) block
+ * (fused_gate_up_swiglu_at and fused_down_combine_at,
+ * moe-fused/src/kernels.metal:400-487; encodeFused with atomicVar,
+ * moe-fused/src/main.mm:176-206): three launches, the router zeroing a
+ * workspace array of sum(h) per slot and 32-element chunk, gate/up adding
+ * every h value to it (as a float, before its fp16 rounding) with a
+ * device-scope atomic, down reading the sums instead of summing h. The sums'
+ * order is not fixed, so y may differ in the last bits from call to call;
+ * idx, wgt and h are those of the other paths. KQ_EUNSUPPORTED unless batch
+ * <= 2 and the streaming kernels take the shapes (the block's default form
+ * there). */
 #define KQ_MOE_PATH_AUTO 0
 #define KQ_MOE_PATH_LAUNCHES 1
 #define KQ_MOE_PATH_ONE 2
+#define KQ_MOE_PATH_ATOMIC 3
 kq_status kq_moe_block_path(const uint8_t* pool, const kq_moe_desc* d,
                             const void* R, kq_dtype r_dtype, const void* X, kq_dtype x_dtype,
                             uint32_t batch, uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H,

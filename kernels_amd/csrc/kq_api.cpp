@@ -329,11 +329,13 @@ kq_status kq_moe_block_path(const uint8_t* pool, const kq_moe_desc* d, const voi
     kq_status st = check_block(pool, d, R, r_dtype, X, x_dtype, batch, idx, wgt, xh, H, Y, y_dtype);
     if (st != KQ_OK) return st;
     if ((st = check_ws(d, batch, ws, ws_bytes)) != KQ_OK) return st;
-    if (path != KQ_MOE_PATH_AUTO && path != KQ_MOE_PATH_LAUNCHES && path != KQ_MOE_PATH_ONE)
+    if (path != KQ_MOE_PATH_AUTO && path != KQ_MOE_PATH_LAUNCHES && path != KQ_MOE_PATH_ONE &&
+        path != KQ_MOE_PATH_ATOMIC)
         return KQ_EINVAL;
     if (path == KQ_MOE_PATH_ONE &&
         !kq::moe_one_supported(*d, batch))
         return KQ_EUNSUPPORTED;
+    if (path == KQ_MOE_PATH_ATOMIC && !kq::moe_atomic_supported(*d, batch)) return KQ_EUNSUPPORTED;
     return hip_status(kq::launch_moe_block(pool, *d, R, r_dtype == KQ_F32, X, x_dtype == KQ_F32,
                                            batch, idx, wgt, xh, H, Y, y_dtype == KQ_F32, ws,
                                            reinterpret_cast<hipStream_t>(stream), path));

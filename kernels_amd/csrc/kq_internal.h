@@ -97,5 +97,7 @@ hipError_t launch_moe_block(const uint8_t* pool, const kq_moe_desc& d, const voi
                             hipStream_t s, int path);
 // The one-launch block's limits (shape, and every workgroup resident at once).
 bool moe_one_supported(const kq_moe_desc& d, uint32_t batch);
+// The atomic sum(h) block's limits (the streaming gate/up and down).
+bool moe_atomic_supported(const kq_moe_desc& d, uint32_t batch);
 
 }  // namespace kq

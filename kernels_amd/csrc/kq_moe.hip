@@ -79,12 +79,13 @@ struct Plan {
 };
 
 struct WsLayout {
-    size_t lg, cnt, plan, sync, tag, ys, total;
+    size_t lg, cnt, plan, sync, tag, ys, xsh, total;
 };
 
 // Workspace: [completion counter, error word][plan][grid-barrier counters]
 // [tagged logits of the one-launch block, kTagCopies x 8 B x 256][logits f32 batch x
-// n_experts][per-slot down products f32 batch x top_k x hidden]. Everything
+// n_experts][per-slot down products f32 batch x top_k x hidden][the atomic
+// block's sum(h) per slot and 32-chunk, f32 batch x top_k x ceil(inter / 32)]. Everything
 // before the logits sits at fixed offsets, the same for every batch and
 // descriptor: a workspace sized for a large batch and reused at a smaller
 // one (or the reverse) never has its counter, plan or barrier state
@@ -105,7 +106,8 @@ WsLayout ws_layout(const kq_moe_desc& d, uint32_t batch) {
     L.tag = kWsTag;
     L.lg = L.tag + kTagCopies * 8 * 256;
     L.ys = L.lg + al(4ull * batch * d.n_experts);
-    L.total = L.ys + al(4ull * batch * d.top_k * d.hidden);
+    L.xsh = L.ys + al(4ull * batch * d.top_k * d.hidden);
+    L.total = L.xsh + al(4ull * batch * d.top_k * ((d.inter + 31) / 32));
     return L;
 }
 
@@ -255,7 +257,8 @@ template <bool RF32, bool XF32, int IT, bool TAIL, int NW>
 __global__ __launch_bounds__(64 * NW) void moe_router_k(
     const void* __restrict__ R, const void* __restrict__ X, uint32_t batch, uint32_t NE,
     uint32_t HID, uint32_t TK, uint16_t* __restrict__ xh, float* lg, uint32_t* cnt,
-    uint32_t* __restrict__ idx_out, float* __restrict__ wgt_out, Plan* __restrict__ plan_out) {
+    uint32_t* __restrict__ idx_out, float* __restrict__ wgt_out, Plan* __restrict__ plan_out,
+    float* __restrict__ xsz = nullptr, uint32_t nxs = 0) {
     constexpr int NBT = 2;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t e = blockIdx.x * (NW) + wave, ec = min(e, NE - 1);
@@ -269,6 +272,11 @@ __global__ __launch_bounds__(64 * NW) void moe_router_k(
 #pragma unroll
         for (int t = 0; t < NBT; ++t)
             x[t][i] = load8<XF32>(X, (size_t)min(t0 + t, batch - 1) * HID + k);
+    }
+    if (xsz) {  // the atomic block's sum(h) accumulators, zeroed as the reference's pass 1 does
+        const uint32_t nthr = gridDim.x * gridDim.y * (64 * NW);
+        for (uint32_t i = (blockIdx.y * gridDim.x + blockIdx.x) * (64 * NW) + tid; i < nxs; i += nthr)
+            xsz[i] = 0.0f;
     }
     if (XF32 && xh) {  // fp16 copy of x for the projections, spread over the grid
         const uint32_t tot = batch * HID, nthr = gridDim.x * gridDim.y * (64 * NW);
@@ -766,12 +774,15 @@ __device__ __forceinline__ void st_stage_load(StStage& st, const uint16_t* src, 
 // 2048 + c0 * 8; chunks past K are zero. The caller synchronises.
 // st_word_store: word w (8 elements) of the staged vectors, every lane of
 // the wave taking part (quad sums), the store only if w < total.
-template <int J>
+// AT: the chunk's sum s comes in sx (the atomic block's sum(h) of the chunk)
+// instead of from the staged values; its offset constant still does.
+template <int J, bool AT = false>
 __device__ __forceinline__ void st_word_store(const u32x4& sv, uint32_t w, uint32_t total,
-                                              unsigned char* act, uint32_t nw) {
+                                              unsigned char* act, uint32_t nw, float sx = 0.0f) {
     float s, c;
     word_consts(sv, s, c);
-    s = quad_sum(s);
+    if constexpr (AT) s = sx;
+    else s = quad_sum(s);
     c = quad_sum(c);
     if (w < total) {
         const uint32_t v = w / nw, wi = w - v * nw, ch = wi >> 2, jw = wi & 3;
@@ -800,6 +811,32 @@ __device__ __forceinline__ void st_stage_store(const StStage& st, unsigned char*
     for (int i = 0; i < kStXr; ++i) {
         if ((uint32_t)i * nthr >= st.total) break;  // uniform
         st_word_store<J>(st.sv[i], i * nthr + tid, st.total, act, nw);
+    }
+    st_pad_store<J>(act, nvec, K);
+}
+// The atomic block's chunk sums for the words a thread stages (vector v,
+// chunk c at xsh[v * ceil(K / 32) + c]), loaded with the staging loads.
+struct StSums {
+    float v[kStXr];
+};
+__device__ __forceinline__ void st_sums_load(StSums& ss, const StStage& st, const float* xsh,
+                                             uint32_t K) {
+    const uint32_t nthr = blockDim.x, tid = threadIdx.x, nw = K >> 3, nq = (K + 31) >> 5;
+#pragma unroll
+    for (int i = 0; i < kStXr; ++i) {
+        if ((uint32_t)i * nthr >= st.total) break;  // uniform
+        const uint32_t w = min(i * nthr + tid, st.total - 1), v = w / nw;
+        ss.v[i] = xsh[v * nq + ((w - v * nw) >> 2)];
+    }
+}
+template <int J>
+__device__ __forceinline__ void st_stage_store_sums(const StStage& st, const StSums& ss,
+                                                    unsigned char* act, uint32_t nvec, uint32_t K) {
+    const uint32_t nthr = blockDim.x, tid = threadIdx.x, nw = K >> 3;
+#pragma unroll
+    for (int i = 0; i < kStXr; ++i) {
+        if ((uint32_t)i * nthr >= st.total) break;  // uniform
+        st_word_store<J, true>(st.sv[i], i * nthr + tid, st.total, act, nw, ss.v[i]);
     }
     st_pad_store<J>(act, nvec, K);
 }
@@ -896,12 +933,19 @@ __device__ __forceinline__ float st_dotx_dq(const StSlot<J>& e, const DequantCon
 // activation chunks stay in registers for the whole stream.
 // SRC: 0 plan from idx, 1 plan from the router, 2 top-k from the router's
 // logits (lg) here, publishing idx / wgt / plan (workgroup 0).
-template <int J, int SRC, bool XREG>
+// AT (the atomic sum(h) block, moe-fused/src/kernels.metal:410-451): every h
+// value, as a float before its fp16 rounding, is also summed into xsh[slot][row
+// / 32] (order-nondeterministic sums): first per workgroup in LDS (ds_add_f32,
+// outside the vector-memory counter the ring waits on), then one device-scope
+// float atomic per (slot, chunk) the workgroup touched, after its stream. (A
+// device atomic per h value, inside the stream, took the block from 21.8 to
+// 29.8 us at one token: each one joined the next ring wait.)
+template <int J, int SRC, bool XREG, bool AT = false>
 __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     const uint8_t* __restrict__ pool, kq_moe_desc d, const uint32_t* __restrict__ idx,
     const Plan* __restrict__ plan_g, const uint16_t* __restrict__ xh, uint16_t* __restrict__ H,
     uint32_t batch, const float* __restrict__ lg, uint32_t* __restrict__ idx_out,
-    float* __restrict__ wgt_out, Plan* __restrict__ plan_out) {
+    float* __restrict__ wgt_out, Plan* __restrict__ plan_out, float* __restrict__ xsh = nullptr) {
     extern __shared__ __align__(16) unsigned char act[];
     __shared__ Plan ps;
     __shared__ uint32_t s_idx[kMaxSlots];
@@ -921,6 +965,20 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     const uint32_t per = (N + gridDim.x - 1) / gridDim.x, k0 = blockIdx.x * per;
     const uint32_t cnt = k0 < N ? min(per, N - k0) : 0;
     const uint32_t nit = cnt > wave ? (cnt - wave + kStWaves - 1) / kStWaves : 0;
+    // AT: the chunks (plan entry u, row / 32) of this workgroup's items are
+    // cg0 .. cg0 + nchw - 1 in cg = u * nq + row / 32; lacc[slot][cg - cg0]
+    // (LDS after the staged x) sums their h values
+    const uint32_t nq = (IN + 31) >> 5, nsl = batch * TK;
+    uint32_t cg0 = 0, nchw = 0;
+    float* lacc = reinterpret_cast<float*>(act + st_act_bytes(batch, K));
+    if constexpr (AT) {
+        if (cnt) {
+            const uint32_t kb = k0 + cnt - 1;
+            cg0 = (k0 / IN) * nq + (k0 % IN) / 32;
+            nchw = (kb / IN) * nq + (kb % IN) / 32 - cg0 + 1;
+        }
+        for (uint32_t i = threadIdx.x; i < nsl * nchw; i += blockDim.x) lacc[i] = 0.0f;
+    }
 
     const StLane<J> L = st_lane<J>(half ? d.off_up : d.off_gate, d, K, 0, 0, 0);
     constexpr int D = 2;
@@ -984,7 +1042,13 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
             if constexpr (XREG) acc = st_dotx<J>(q, xr);
             else acc = st_dot<J>(q, act, s / TK);
             const float2 hs = half_sums(acc);
-            const uint16_t hv = f2h(swiglu(hs.x + bg, hs.y + bu));
+            const float hf = swiglu(hs.x + bg, hs.y + bu);
+            const uint16_t hv = f2h(hf);
+            if constexpr (AT) {
+                if (lane == 0)
+                    __hip_atomic_fetch_add(lacc + s * nchw + (cc.u * nq + (cc.i >> 5) - cg0), hf,
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
             if (lane >= k) {
                 oi = (size_t)s * IN + cc.i;
                 ov = hv;
@@ -1004,17 +1068,31 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     }
 #pragma unroll
     for (int s = 0; s < D; ++s) step(ring[s], it + s, true);
+    if constexpr (AT) {  // every wave's LDS sums done; waves without items (wave >= cnt) have left
+        __syncthreads();
+        const uint32_t nact = 64 * min(cnt, (uint32_t)kStWaves);
+        for (uint32_t i = threadIdx.x; i < nsl * nchw; i += nact) {
+            const float v = lacc[i];
+            const uint32_t sl = i / nchw, cg = cg0 + (i - sl * nchw);
+            if (v != 0.0f)  // only (slot, chunk) pairs of this workgroup's items hold sums
+                __hip_atomic_fetch_add(xsh + (size_t)sl * nq + cg % nq, v, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
 // Down + weighted combine: workgroup w owns output row pairs [p0, p1) for
 // every distinct expert; items are (u, pair) in u-major order. Per-slot
 // wgt * (down . h + bias) goes to LDS and the slots are summed in k order
 // after the stream (deterministic, no atomics).
-template <int J, bool FROM_PLAN>
+// AT (the atomic sum(h) block, moe-fused/src/kernels.metal:453-487): the
+// chunk sums of h come from xsh, which the gate/up launch accumulated.
+template <int J, bool FROM_PLAN, bool AT = false>
 __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
     const uint8_t* __restrict__ pool, kq_moe_desc d, const uint32_t* __restrict__ idx,
     const float* __restrict__ wgt, const Plan* __restrict__ plan_g,
-    const uint16_t* __restrict__ H, void* __restrict__ Y, int y_f32, uint32_t batch, uint32_t pp) {
+    const uint16_t* __restrict__ H, void* __restrict__ Y, int y_f32, uint32_t batch, uint32_t pp,
+    const float* __restrict__ xsh = nullptr) {
     extern __shared__ __align__(16) unsigned char act[];  // [nslots h blocks][ys]
     __shared__ Plan ps;
     __shared__ uint32_t s_idx[kMaxSlots];
@@ -1028,6 +1106,8 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
 
     StStage st;
     st_stage_load(st, H, nslots, K);
+    StSums ss;
+    if constexpr (AT) st_sums_load(ss, st, xsh, K);
     // From the workspace plan, every wave reads the plan and the weights
     // itself at uniform addresses (scalar loads): no LDS copy and no barrier,
     // so the h staging loads stay in flight while the ring is primed.
@@ -1085,7 +1165,8 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
         issue(ring[s]);
         __builtin_amdgcn_sched_barrier(0);
     }
-    st_stage_store<J>(st, act, nslots, K);
+    if constexpr (AT) st_stage_store_sums<J>(st, ss, act, nslots, K);
+    else st_stage_store<J>(st, act, nslots, K);
     __syncthreads();
 
     const DequantConsts kc;
@@ -1918,6 +1999,8 @@ struct RtOut {
     float* lg;
     uint32_t* cnt;
     Plan* plan;
+    float* xsz = nullptr;  // zeroed by the router (the atomic block's sum(h)), nxs floats
+    uint32_t nxs = 0;
 };
 
 template <int IT, bool TAIL>
@@ -1934,7 +2017,8 @@ hipError_t launch_router_it(const void* R, bool r_f32, const void* X, bool x_f32
     Plan* plan = o.plan;
 #define KQ_RT(RF, XF)                                                                     \
     moe_router_k<RF, XF, IT, TAIL, NW><<<grid, 64 * NW, 0, s>>>(R, X, batch, d.n_experts, d.hidden, \
-                                                         d.top_k, xh, lg, cnt, idx, wgt, plan)
+                                                         d.top_k, xh, lg, cnt, idx, wgt, plan,  \
+                                                         o.xsz, o.nxs)
     if (r_f32 && x_f32) KQ_RT(true, true);
     else if (r_f32) KQ_RT(true, false);
     else if (x_f32) KQ_RT(false, true);
@@ -1957,11 +2041,15 @@ hipError_t launch_router_o(const void* R, bool r_f32, const void* X, bool x_f32,
 template <bool TAIL>
 hipError_t launch_router_t(const void* R, bool r_f32, const void* X, bool x_f32, uint32_t batch,
                            const kq_moe_desc& d, uint16_t* xh, void* ws, uint32_t* idx, float* wgt,
-                           hipStream_t s) {
+                           hipStream_t s, bool zero_xsh = false) {
     const WsLayout L = ws_layout(d, batch);
     uint8_t* w = reinterpret_cast<uint8_t*>(ws);
-    const RtOut o{reinterpret_cast<float*>(w + L.lg), reinterpret_cast<uint32_t*>(w + L.cnt),
-                  reinterpret_cast<Plan*>(w + L.plan)};
+    RtOut o{reinterpret_cast<float*>(w + L.lg), reinterpret_cast<uint32_t*>(w + L.cnt),
+            reinterpret_cast<Plan*>(w + L.plan)};
+    if (zero_xsh) {
+        o.xsz = reinterpret_cast<float*>(w + L.xsh);
+        o.nxs = batch * d.top_k * ((d.inter + 31) / 32);
+    }
     return launch_router_o<TAIL>(R, r_f32, X, x_f32, batch, d, xh, o, idx, wgt, s);
 }
 
@@ -1998,6 +2086,17 @@ bool st_ok(const kq_moe_desc& d, uint32_t nvec, uint32_t K, size_t extra) {
            st_act_bytes(nvec, K) + extra + kStStatic <= kLdsMax;
 }
 
+// The atomic block's per-workgroup sums of h in the streaming gate/up's LDS:
+// slots x the chunks a workgroup's items can span -- per = its share of at
+// most batch x top_k experts' rows spans at most per / 32 + 2 chunks of one
+// expert plus one per expert boundary (at most per / inter + 1), one more for
+// rounding.
+size_t gu_sums_lds(const kq_moe_desc& d, uint32_t batch) {
+    const uint32_t nsl = batch * d.top_k, G = cu_count();
+    const uint32_t per = (nsl * d.inter + G - 1) / G;
+    return (size_t)nsl * (per / 32 + 4 + per / d.inter) * 4;
+}
+
 // Top-k in the gate/up launch (SRC 2): the logits, and where idx / wgt /
 // plan go.
 struct GuTopk {
@@ -2007,32 +2106,33 @@ struct GuTopk {
     Plan* plan;
 };
 
-template <int J, int SRC>
+template <int J, int SRC, bool AT = false>
 hipError_t go_gu_st(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
                     const Plan* plan, const uint16_t* xh, uint16_t* H, uint32_t batch,
-                    GuTopk tk, hipStream_t s) {
-    const size_t lds = st_act_bytes(batch, d.hidden);
+                    GuTopk tk, hipStream_t s, float* xsh = nullptr) {
+    const uint32_t G = cu_count();
+    const size_t lds = st_act_bytes(batch, d.hidden) + (AT ? gu_sums_lds(d, batch) : 0);
     auto run = [&](auto kern) {
         const hipError_t e = st_lds(kern, lds);
         if (e != hipSuccess) return e;
-        kern<<<cu_count(), 64 * kStWaves, lds, s>>>(pool, d, idx, plan, xh, H, batch, tk.lg,
-                                                     tk.idx, tk.wgt, tk.plan);
+        kern<<<G, 64 * kStWaves, lds, s>>>(pool, d, idx, plan, xh, H, batch, tk.lg,
+                                            tk.idx, tk.wgt, tk.plan, xsh);
         return hipGetLastError();
     };
-    return batch == 1 ? run(moe_gu_stream_k<J, SRC, true>) : run(moe_gu_stream_k<J, SRC, false>);
+    return batch == 1 ? run(moe_gu_stream_k<J, SRC, true, AT>) : run(moe_gu_stream_k<J, SRC, false, AT>);
 }
 
-template <int J, bool FP>
+template <int J, bool FP, bool AT = false>
 hipError_t go_dn_st(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
                     const float* wgt, const Plan* plan, const uint16_t* H, void* Y, bool y_f32,
-                    uint32_t batch, uint32_t pp, hipStream_t s) {
-    auto kern = moe_dn_stream_k<J, FP>;
+                    uint32_t batch, uint32_t pp, hipStream_t s, const float* xsh = nullptr) {
+    auto kern = moe_dn_stream_k<J, FP, AT>;
     const uint32_t nslots = batch * d.top_k, npairs = d.hidden / 2;
     const size_t lds = st_act_bytes(nslots, d.inter) + (size_t)nslots * 2 * pp * 4;
     const hipError_t e = st_lds(kern, lds);
     if (e != hipSuccess) return e;
     kern<<<(npairs + pp - 1) / pp, 64 * kStWaves, lds, s>>>(pool, d, idx, wgt, plan, H, Y,
-                                                             y_f32 ? 1 : 0, batch, pp);
+                                                             y_f32 ? 1 : 0, batch, pp, xsh);
     return hipGetLastError();
 }
 
@@ -2043,15 +2143,15 @@ bool gu_streams(const kq_moe_desc& d, uint32_t batch) {
     return batch <= 2 && st_ok(d, batch, d.hidden, 0);
 }
 
-template <int SRC>
+template <int SRC, bool AT = false>
 hipError_t launch_gu_st(const uint8_t* pool, const kq_moe_desc& d, const uint32_t* idx,
                         const Plan* plan, const uint16_t* xh, uint16_t* H, uint32_t batch,
-                        GuTopk tk, hipStream_t s) {
+                        GuTopk tk, hipStream_t s, float* xsh = nullptr) {
     switch (chunks_j(d.hidden)) {
-        case 1: return go_gu_st<1, SRC>(pool, d, idx, plan, xh, H, batch, tk, s);
-        case 2: return go_gu_st<2, SRC>(pool, d, idx, plan, xh, H, batch, tk, s);
-        case 3: return go_gu_st<3, SRC>(pool, d, idx, plan, xh, H, batch, tk, s);
-        case 4: return go_gu_st<4, SRC>(pool, d, idx, plan, xh, H, batch, tk, s);
+        case 1: return go_gu_st<1, SRC, AT>(pool, d, idx, plan, xh, H, batch, tk, s, xsh);
+        case 2: return go_gu_st<2, SRC, AT>(pool, d, idx, plan, xh, H, batch, tk, s, xsh);
+        case 3: return go_gu_st<3, SRC, AT>(pool, d, idx, plan, xh, H, batch, tk, s, xsh);
+        case 4: return go_gu_st<4, SRC, AT>(pool, d, idx, plan, xh, H, batch, tk, s, xsh);
         default: return hipErrorInvalidValue;
     }
 }
@@ -2280,6 +2380,15 @@ hipError_t scratch_ptr(void** out, hipStream_t s) {
 
 }  // namespace
 
+// The atomic sum(h) block: the streaming gate/up (1-2 tokens) and the
+// streaming down, whose staging takes the sums.
+bool moe_atomic_supported(const kq_moe_desc& d, uint32_t batch) {
+    if (!gu_streams(d, batch) || chunks_j(d.inter) < 1 || chunks_j(d.inter) > 4) return false;
+    if (!st_ok(d, batch, d.hidden, gu_sums_lds(d, batch))) return false;
+    const uint32_t nslots = batch * d.top_k, pp = (d.hidden / 2 + cu_count() - 1) / cu_count();
+    return st_ok(d, nslots, d.inter, (size_t)nslots * 2 * pp * 4);
+}
+
 bool moe_one_supported(const kq_moe_desc& d, uint32_t batch) {
     return one_fits(d, batch) && one_resident(one_kern(chunks_j(d.hidden)), one_lds(d));
 }
@@ -2346,6 +2455,22 @@ hipError_t launch_moe_block(const uint8_t* pool, const kq_moe_desc& d, const voi
     Plan* plan = reinterpret_cast<Plan*>(w + L.plan);
     const uint16_t* xin = x_f32 ? xh : reinterpret_cast<const uint16_t*>(X);
     hipError_t e;
+    if (path == KQ_MOE_PATH_ATOMIC) {  // callers check moe_atomic_supported
+        float* xsh = reinterpret_cast<float*>(w + L.xsh);
+        e = launch_router_t<false>(R, r_f32, X, x_f32, batch, d, xh, ws, idx, wgt, s, true);
+        if (e != hipSuccess) return e;
+        const GuTopk tk{reinterpret_cast<const float*>(w + L.lg), idx, wgt, plan};
+        e = launch_gu_st<2, true>(pool, d, idx, plan, xin, H, batch, tk, s, xsh);
+        if (e != hipSuccess) return e;
+        const uint32_t pp = (d.hidden / 2 + cu_count() - 1) / cu_count();
+        switch (chunks_j(d.inter)) {
+            case 1: return go_dn_st<1, true, true>(pool, d, idx, wgt, plan, H, Y, y_f32, batch, pp, s, xsh);
+            case 2: return go_dn_st<2, true, true>(pool, d, idx, wgt, plan, H, Y, y_f32, batch, pp, s, xsh);
+            case 3: return go_dn_st<3, true, true>(pool, d, idx, wgt, plan, H, Y, y_f32, batch, pp, s, xsh);
+            case 4: return go_dn_st<4, true, true>(pool, d, idx, wgt, plan, H, Y, y_f32, batch, pp, s, xsh);
+            default: return hipErrorInvalidValue;
+        }
+    }
     if (gu_streams(d, batch)) {
         e = launch_router_t<false>(R, r_f32, X, x_f32, batch, d, xh, ws, idx, wgt, s);
         if (e != hipSuccess) return e;

@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(HERE, "_lib", "libkq.so")
 KQ_OK, KQ_EINVAL, KQ_ENULL, KQ_EALIGN, KQ_EUNSUPPORTED, KQ_EWORKSPACE, KQ_EHIP = range(7)
 F16, BF16, F32 = 0, 1, 2
 PATH_AUTO, PATH_VALU, PATH_MFMA, PATH_SCALAR = 0, 1, 2, 3
-MOE_PATH_AUTO, MOE_PATH_LAUNCHES, MOE_PATH_ONE = 0, 1, 2  # KQ_MOE_PATH_*
+MOE_PATH_AUTO, MOE_PATH_LAUNCHES, MOE_PATH_ONE, MOE_PATH_ATOMIC = 0, 1, 2, 3  # KQ_MOE_PATH_*
 MOE_WS_ERR_OFFSET = 128  # KQ_MOE_WS_ERR_OFFSET
 
 # every symbol include/kq.h declares
@@ -283,7 +283,9 @@ def moe_block(pool, desc, R, x, idx, wgt, H, y, ws, ws_bytes, batch=1, xh=None, 
               path=None):
     """encodeFused (moe-fused/src/main.mm:176-206): router_topk ->
     gate_up_swiglu -> down_combine on one stream. path (MOE_PATH_*): the
-    launch structure (None: kq_moe_block, the same as MOE_PATH_AUTO)."""
+    launch structure (None: kq_moe_block, the same as MOE_PATH_AUTO);
+    MOE_PATH_ATOMIC is the reference's atomic sum(h) form at 1-2 tokens
+    (moe-fused/src/kernels.metal:400-487)."""
     if path is None:
         _check(lib().kq_moe_block(_ptr(pool), C.byref(desc), _ptr(R), _dt(R), _ptr(x), _dt(x),
                                   batch, _ptr(idx), _ptr(wgt), _ptr(xh), _ptr(H), _ptr(y), _dt(y),

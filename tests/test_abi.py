@@ -101,11 +101,11 @@ def test_moe_desc_and_workspace():
 
 
 def test_moe_workspace_head_is_batch_independent():
-    """The workspace is [counter + plan head][logits][per-slot products]: the
-    batch-dependent parts are exactly the logits and the products, so the
-    head (the router's completion counter and the plan, which must survive
-    between calls) sits at the same offsets for every batch and descriptor,
-    and a workspace sized for one batch can serve another."""
+    """The workspace is [counter + plan head][logits][per-slot products][sums
+    of h for the atomic block]: the batch-dependent parts are exactly those
+    three, so the head (the router's completion counter and the plan, which
+    must survive between calls) sits at the same offsets for every batch and
+    descriptor, and a workspace sized for one batch can serve another."""
     def al(v):
         return (v + 255) // 256 * 256
 
@@ -115,7 +115,7 @@ def test_moe_workspace_head_is_batch_independent():
         d.n_experts, d.top_k = ne, tk
         for b in range(1, 17):
             n = kq.moe_workspace_size(d, b)
-            heads.add(n - al(4 * b * ne) - al(4 * b * tk * d.hidden))
+            heads.add(n - al(4 * b * ne) - al(4 * b * tk * d.hidden) - al(4 * b * tk * ((d.inter + 31) // 32)))
     assert len(heads) == 1, heads
 
 
@@ -168,7 +168,8 @@ def test_moe_rejects_on_host():
 
 def test_moe_block_path_rejects_on_host():
     """kq_moe_block_path: an unknown path is KQ_EINVAL, the one-launch path
-    outside its limits (here two tokens) KQ_EUNSUPPORTED, before any launch."""
+    outside its limits (here two tokens) and the atomic sum(h) path outside
+    its (here three tokens) KQ_EUNSUPPORTED, before any launch."""
     L = kq.lib()
     d = kq.moe_default_desc()
     n = kq.moe_workspace_size(d, 2)
@@ -176,9 +177,12 @@ def test_moe_block_path_rejects_on_host():
     def call(batch, path):
         return L.kq_moe_block_path(FAKE, C.byref(d), FAKE, kq.F16, FAKE, kq.F16, batch, FAKE, FAKE,
                                    None, FAKE, FAKE, kq.F32, FAKE, n, path, None)
-    assert call(1, 3) == kq.KQ_EINVAL
+    assert call(1, 4) == kq.KQ_EINVAL
     assert call(1, -1) == kq.KQ_EINVAL
     assert call(2, kq.MOE_PATH_ONE) == kq.KQ_EUNSUPPORTED
+    n3 = kq.moe_workspace_size(d, 3)
+    assert L.kq_moe_block_path(FAKE, C.byref(d), FAKE, kq.F16, FAKE, kq.F16, 3, FAKE, FAKE, None, FAKE,
+                               FAKE, kq.F32, FAKE, n3, kq.MOE_PATH_ATOMIC, None) == kq.KQ_EUNSUPPORTED
 
 
 def test_moe_unfused_rejects_on_host():

@@ -221,6 +221,71 @@ def test_block_expert_partitioned_down(gpu, pool16, batch):
         assert inf_rel(got, Yref) < 2e-3
 
 
+def _atomic_vs_default(gpu, pool, host, d, R, X, batch, k, what):
+    """The atomic sum(h) block against the default block and the oracle:
+    routing bit for bit; h within one fp16 ulp (the default kernel rounds the
+    SwiGLU's last product straight to fp16, the atomic one also needs it as
+    a float and rounds twice, as the reference's half(hv) does); y to the
+    block's tolerance (its sums of h are fp32 atomics in no fixed order).
+    Two calls on one workspace: the router zeroes the sums every call."""
+    oidx, owgt, lg = oracle.moe_router(R, oracle.F16, X, oracle.F16, batch, odesc(d))
+    assert routing_margin(lg, k) > 1e-5
+    _, _, Yref = oracle.moe_block(host, odesc(d), R, oracle.F16, X, oracle.F16, batch)
+    Rd, Xd = dev(R, gpu).view(torch.float16), dev(X, gpu).view(torch.float16)
+    ref, at = Block(gpu, d, batch), Block(gpu, d, batch)
+    kq.moe_block(pool, d, Rd, Xd, ref.idx, ref.wgt, ref.H, ref.y, ref.ws, ref.wsb, batch=batch)
+    torch.cuda.synchronize()
+    for rep in range(2):
+        at.y.fill_(float("nan"))
+        at.H.zero_()
+        kq.moe_block(pool, d, Rd, Xd, at.idx, at.wgt, at.H, at.y, at.ws, at.wsb, batch=batch,
+                     path=kq.MOE_PATH_ATOMIC)
+        torch.cuda.synchronize()
+        assert np.array_equal(at.idx.cpu().numpy().astype(np.uint32), oidx), f"{what} rep {rep}"
+        assert torch.equal(at.wgt, ref.wgt), f"{what} rep {rep}"
+        ulp = (at.H.view(torch.int16).int() - ref.H.view(torch.int16).int()).abs()
+        assert int(ulp.max()) <= 1, f"{what} rep {rep}: h {int(ulp.max())} ulp from the default block"
+        assert float((ulp != 0).float().mean()) < 0.01, f"{what} rep {rep}"
+        got = to_f64(at.y)
+        assert_close(got, Yref, what=f"{what} rep {rep}")
+        assert inf_rel(got, Yref) < 2e-3
+        assert inf_rel(got, to_f64(ref.y)) < 1e-3, f"{what} rep {rep}: far from the default block"
+
+
+@pytest.mark.parametrize("batch", [1, 2])
+def test_block_atomic_sum_h(gpu, pool16, batch):
+    """KQ_MOE_PATH_ATOMIC at gpt-oss shapes (16 experts, top-4), 1 and 2
+    tokens (moe-fused/src/kernels.metal:400-487)."""
+    host, pool = pool16
+    d = _pool_desc(16)
+    R, X = gen.moe_inputs(16, batch=batch, seed=60 + batch)
+    _atomic_vs_default(gpu, pool, host, d, R, X, batch, 4, f"atomic batch {batch}")
+
+
+@pytest.mark.parametrize("hidden,inter,batch", [(1024, 2048, 1), (4096, 512, 2), (2048, 4096, 1)])
+def test_block_atomic_sum_h_other_shapes(gpu, hidden, inter, batch):
+    """KQ_MOE_PATH_ATOMIC on other descriptors (chunk counts 1-4 of both
+    streaming kernels, partial chunks, top-3)."""
+    d, off = _compact_desc(hidden, inter, 16, 3)
+    host = gen.moe_pool(16, seed=hidden + inter + 7, quantize=True, hidden=hidden, inter=inter,
+                        blob=d.blob, off=off)
+    R, X = gen.moe_inputs(16, hidden=hidden, batch=batch, seed=inter + batch + 7)
+    _atomic_vs_default(gpu, dev(host, gpu), host, d, R, X, batch, 3, f"atomic {hidden}x{inter} b{batch}")
+
+
+def test_block_atomic_unsupported(gpu, pool16):
+    """Three tokens: the streaming gate/up does not run, so the atomic path is
+    refused (KQ_EUNSUPPORTED) rather than run in another form."""
+    host, pool = pool16
+    d = _pool_desc(16)
+    R, X = gen.moe_inputs(16, batch=3, seed=70)
+    b = Block(gpu, d, 3)
+    with pytest.raises(kq.KQError) as e:
+        kq.moe_block(pool, d, dev(R, gpu).view(torch.float16), dev(X, gpu).view(torch.float16), b.idx,
+                     b.wgt, b.H, b.y, b.ws, b.wsb, batch=3, path=kq.MOE_PATH_ATOMIC)
+    assert e.value.status == kq.KQ_EUNSUPPORTED
+
+
 def test_workspace_reused_across_batches(gpu, pool16):
     """One workspace sized for 16 tokens serves calls at 8, 3, 16 and 1 tokens
     in turn (every block form: streaming, expert-partitioned gate/up and
