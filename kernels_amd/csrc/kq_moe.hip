@@ -1226,12 +1226,15 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
 // loads plan entries l and l + 64 with vector loads (one round trip), a
 // wave prefix sum gives every C_u, a ballot finds b's entry, and its expert
 // and slot masks come back by readlane.
-// Costs measured at 8 tokens: a row of a two-slot expert took 1.45x the
-// time of a one-slot row. Ring depth 3 (long per-wave streams here, ~40
-// items): against depth 4, 4 / 8 / 16 tokens 53.9 / 92.8 / 166.0 ->
+// Costs: a row's weights 4, each slot's dot product 5 (a two-slot row 1.56x a
+// one-slot row). Swept with the 3-deep ring, slot weight 2 / 3 / 4 / 5 / 8 /
+// 11 against row weight 4: 4 tokens 52.5 / 52.2 / 51.9 / 51.5 / 51.6 / 51.8,
+// 8 tokens 93.7 / 89.4 / 88.5 / 88.5 / 89.1 / 89.3, 16 tokens 174.9 / 163.9 /
+// 159.7 / 158.8 / 158.7 / 158.6 us per block.
+// Ring depth 3 (long per-wave streams here, ~40 items): against depth 4, 4 / 8 / 16 tokens 53.9 / 92.8 / 166.0 ->
 // 52.2 / 89.4 / 163.1 us per block (depth 4 held the one-slot gate/up at
 // 256 VGPRs with 3 spilled; depth 2: 51.3 / 89.9 / 166.1).
-constexpr uint32_t kPartRow = 4, kPartSlot = 3;
+constexpr uint32_t kPartRow = 4, kPartSlot = 5;
 constexpr int kPartD = 3;
 struct PartAssign {
     uint32_t u, r0, nr, ex;  // u = 0xFFFFFFFF: no work for this workgroup
