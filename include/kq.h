@@ -100,8 +100,8 @@ kq_status kq_int4_gemv_path(const uint32_t* W, const void* S, const void* B, kq_
  * VALU: rows = K parts P per workgroup (a divisor of the number of 2048-k
  * steps), unroll = ring depth D (2, 4, 8).
  * MFMA: rows = K parts P per workgroup (a divisor of K/128; at most 8 with
- * 2 or 4 tiles per wave, else 16), unroll = 2 (the ring depth) or 10 * T + 2
- * with T the 16-row tiles per wave (1, 2, 4).
+ * 2 or 4 tiles per wave, else 16), unroll = 10 * T + D with T the 16-row
+ * tiles per wave and D its ring depth in steps: 12, 24 or 42.
  * Returns KQ_EUNSUPPORTED for a shape the family cannot run. Used by the
  * benchmark sweeps and the tests. */
 kq_status kq_int4_gemv_cfg(const uint32_t* W, const void* S, const void* B, kq_dtype sb_dtype,

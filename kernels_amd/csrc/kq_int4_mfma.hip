@@ -22,15 +22,15 @@ constexpr size_t kLdsMax = 160 * 1024;
 bool make_plan(uint32_t M, uint32_t K, uint32_t G, uint32_t ntok, Int4Cfg cfg, mfma::Plan& out) {
     (void)ntok;
     const uint32_t nspan = K / 128, ntiles = (M + mfma::kTile - 1) / mfma::kTile, cu = cu_count();
-    // cfg.unroll: 0 = automatic, or 10 * T + 2 (ring depth 2); cfg.rows: K parts P (0 = automatic)
+    // cfg.unroll: 0 = automatic, or 10 * T + T's ring depth (12, 24, 42);
+    // cfg.rows: K parts P (0 = automatic)
     uint32_t fT = 0;
-    if (cfg.unroll >= 10) {
+    if (cfg.unroll != 0) {
         fT = (uint32_t)cfg.unroll / 10;
-        if (cfg.unroll % 10 != 2) return false;
-    } else if (cfg.unroll != 0 && cfg.unroll != 2) {
-        return false;
+        if (cfg.unroll < 0 || (fT != 1 && fT != 2 && fT != 4) ||
+            (uint32_t)cfg.unroll % 10 != (uint32_t)mfma::ring_depth(fT))
+            return false;
     }
-    if (fT && fT != 1 && fT != 2 && fT != 4) return false;
     bool found = false;
     double best = 0.0;
     for (uint32_t T : {4u, 2u, 1u}) {
@@ -54,7 +54,8 @@ bool make_plan(uint32_t M, uint32_t K, uint32_t G, uint32_t ntok, Int4Cfg cfg, m
             if (lds > kLdsMax) continue;
             // padding steps move no bytes but take issue slots
             const double steps = rounds * J + 0.3 * (nsteps - rounds * J);
-            const double inflight = (double)waves * 2 * T;  // KiB per CU
+            // KiB per CU: D/2 span pairs of T 2-KiB tiles per wave
+            const double inflight = (double)waves * mfma::ring_depth(T) * T;
             const double cost = (double)((nwg + cu - 1) / cu) * waves * steps * T *
                                 (inflight < 48.0 ? 48.0 / inflight : 1.0) * (P > 1 ? 1.02 : 1.0);
             if (!found || cost < best) {

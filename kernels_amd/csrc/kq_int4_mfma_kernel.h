@@ -57,7 +57,8 @@
 // since per-span loads of 2-16 bytes from 16 rows cost more than the weights.
 //
 // Pipelining: each wave streams its (row group, span) steps through a ring of
-// two register slots. Every load is unconditional: rows past the end are
+// D register slots (ring_depth: 4 at two tiles a wave, else 2; an even slot
+// also holds its span pair's weights). Every load is unconditional: rows past the end are
 // clamped to valid addresses (results discarded), and padding steps (a part
 // padded to whole windows, the last round padded to the loop body) load out
 // of the descriptors' range -- zeros, which add exactly nothing, and no
@@ -101,6 +102,13 @@ struct Plan {
 __host__ __device__ constexpr uint32_t max_waves(uint32_t G, uint32_t T) {
     return T >= 2 || G == 32 ? 8 : 16;
 }
+
+// Ring depth in steps (even: a step pair shares one weight load). Two tiles
+// a wave have the registers for two span pairs ahead (198 VGPRs of 256);
+// four tiles (202 at depth 2) and one tile at 16 waves (116 of 128) do not.
+// Depth 4 at two tiles, with the planner counting its loads in flight:
+// 8192x28672 at 16 tokens 42.3 -> 40.6 us, 14336x4096 26.5 -> 20.1 us.
+__host__ __device__ constexpr int ring_depth(uint32_t T) { return T == 2 ? 4 : 2; }
 
 __host__ __device__ inline size_t lds_part(uint32_t waves, uint32_t T, uint32_t rounds, uint32_t P) {
     return P > 1 ? (size_t)(rounds > 1 ? 2 : 1) * waves * T * 4 * 64 * 4 : 0;
@@ -354,7 +362,7 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
     constexpr int NP = (NG + 1) / 2;     // group pairs (correction MFMAs) per span
     constexpr int PER = 4 / NG;          // MFMAs per group
     constexpr uint32_t MB = SB ? 4 : 2;  // meta bytes per group (per array)
-    constexpr int D = 2;                 // ring depth (steps)
+    constexpr int D = ring_depth(T);     // ring depth (steps)
     constexpr int U = 2 * kWin;          // steps per loop body (two meta windows)
 
 
@@ -419,12 +427,15 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
     // nothing (x = 0 and scale/bias = 0), and cost no memory traffic.
     // named buffers, not arrays: arrays of these (selected by constant
     // indices after unrolling) have been kept in scratch by the compiler
-    SlotE<T> ring0;
-    SlotO ring1;
+    SlotE<T> ring0, ring2;
+    SlotO ring1, ring3;
     MWin<NG, SB> mwa[T], mwb[T];
     auto slot = [&](auto k) __attribute__((always_inline)) -> auto& {
-        if constexpr (decltype(k)::value == 0) return ring0;
-        else return ring1;
+        constexpr int kk = decltype(k)::value;
+        if constexpr (kk == 0) return ring0;
+        else if constexpr (kk == 1) return ring1;
+        else if constexpr (kk == 2) return ring2;
+        else return ring3;
     };
     auto mwin = [&](auto b) __attribute__((always_inline)) -> MWin<NG, SB>* {
         if constexpr (decltype(b)::value == 0) return mwa;
@@ -463,12 +474,12 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
             e.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rX, xvo[j] + oob, span * 256, 0);
     };
     Cursor ci{0, 0};
-    issue(ring0, ci, std::integral_constant<int, 0>{});
-    ci.advance(A.J8);
-    __builtin_amdgcn_sched_barrier(0);
-    issue(ring1, ci, std::integral_constant<int, -1>{});
-    ci.advance(A.J8);
-    __builtin_amdgcn_sched_barrier(0);
+    static_for<D>([&](auto kk) __attribute__((always_inline)) {
+        constexpr int k = decltype(kk)::value;
+        issue(slot(kk), ci, std::integral_constant<int, k % kWin == 0 ? (k / kWin) % 2 : -1>{});
+        ci.advance(A.J8);
+        __builtin_amdgcn_sched_barrier(0);
+    });
 
     // ---- per-lane constants
     const DequantConsts kc;
@@ -544,33 +555,49 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
         f16x8 xa[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) xa[j] = xperm(e.x[j]);
+        // Phases over all tiles, so that each tile's MFMA results are not
+        // read until the other tiles' dequant and MFMAs have been issued:
+        // LDS reads and meta, then dequant + group MFMAs, then epilogues.
+        u32x4 wv[T];
+        Meta<NG, SB> m[T];
+#pragma unroll
+        for (int i = 0; i < T; ++i) {
+            wv[i] = *reinterpret_cast<const u32x4*>(wst + i * 2048 + rdo[SP]);
+            m[i] = meta_at<NG, SB, RW>(mwin(std::integral_constant<int, B>{})[i], ba[RW / 2]);
+        }
         f32x4 sums{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < 4; ++j) sums = mma16(ac[j / PER], xa[j], sums);
+        f32x4 dg[T][NG];
+        // tile e's epilogue follows tile e + S's MFMAs; S = T - 1 measured
+        // best (S = 0, 1 and T - 1 compared; 1-3% over S = 0)
+        constexpr int S = T - 1;
+        static_for<T + S>([&](auto ii) __attribute__((always_inline)) {
+            constexpr int i = decltype(ii)::value;
+            if constexpr (i < T) {
+                uint32_t w[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+                regroup<GM>(w);
 #pragma unroll
-        for (int i = 0; i < T; ++i) {
-            const Meta<NG, SB> m = meta_at<NG, SB, RW>(mwin(std::integral_constant<int, B>{})[i], ba[RW / 2]);
-            const u32x4 wv = *reinterpret_cast<const u32x4*>(wst + i * 2048 + rdo[SP]);
-            uint32_t w[4] = {wv.x, wv.y, wv.z, wv.w};
-            regroup<GM>(w);
-            f32x4 dg[NG];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int gi = j / PER;
-                const f32x4 cin = (j % PER == 0) ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : dg[gi];
-                dg[gi] = mma16(xa[j], dq(w[j], kc), cin);
+                for (int j = 0; j < 4; ++j) {
+                    const int gi = j / PER;
+                    const f32x4 cin = (j % PER == 0) ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : dg[i][gi];
+                    dg[i][gi] = mma16(xa[j], dq(w[j], kc), cin);
+                }
             }
+            if constexpr (i >= S) {
+                constexpr int e = i - S;
 #pragma unroll
-            for (int gi = 0; gi < NG; ++gi) {
-                const float sc = sval<NG, SB, BF>(m, gi);
+                for (int gi = 0; gi < NG; ++gi) {
+                    const float sc = sval<NG, SB, BF>(m[e], gi);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(sc, dg[gi][r], acc[i][r]);
+                    for (int r = 0; r < 4; ++r) acc[e][r] = fmaf(sc, dg[e][gi][r], acc[e][r]);
+                }
+#pragma unroll
+                for (int pp = 0; pp < NP; ++pp)
+                    acc[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                        sums[pp], bcorr<NG, SB, BF>(m[e], pp, hi_grp, want_s, shs, hsel), acc[e], 0, 0, 0);
             }
-#pragma unroll
-            for (int pp = 0; pp < NP; ++pp)
-                acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                    sums[pp], bcorr<NG, SB, BF>(m, pp, hi_grp, want_s, shs, hsel), acc[i], 0, 0, 0);
-        }
+        });
         if (c.round < A.rounds && c.j == A.J8 - 1) finish(c.round);
     };
 

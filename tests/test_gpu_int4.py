@@ -133,8 +133,8 @@ def test_forced_kparts_many_rounds(gpu, parts, depth, batch):
     check(got, ref_int4(p), f"P={parts} D={depth} M=9000 b={batch}")
 
 
-# (K parts P, 10 * tiles per wave T + ring depth 2)
-MFMA_PLANS = [(16, 12), (1, 12), (8, 22), (2, 22), (4, 42), (8, 42), (1, 42), (4, 2)]
+# (K parts P, 10 * tiles per wave T + ring depth: 2 at T = 1 and 4, 4 at T = 2; 0 = automatic T)
+MFMA_PLANS = [(16, 12), (1, 12), (8, 24), (2, 24), (4, 42), (8, 42), (1, 42), (4, 0)]
 
 
 @pytest.mark.parametrize("parts,unroll", MFMA_PLANS)
@@ -150,6 +150,20 @@ def test_mfma_forced_plans_agree(gpu, parts, unroll, M, batch):
     check(got, ref_int4(p), f"mfma P={parts} T,D={unroll} M={M} b={batch}")
 
 
+@pytest.mark.parametrize("G", [32, 128])
+@pytest.mark.parametrize("layout", ["sb", "split"])
+@pytest.mark.parametrize("parts", [1, 8])
+def test_mfma_two_tiles_deep_ring(gpu, G, layout, parts):
+    """Two tiles a wave stream through a 4-deep ring (two span pairs ahead,
+    the scale/bias window loaded 4 steps before its first span): other group
+    sizes, both scale/bias layouts, 16 tokens, padding steps (P = 8: 4 spans
+    per part, padded to 8) and two rounds per workgroup (P = 8: one row-group
+    lane)."""
+    p = gen.int4_problem(9000, 4096, G, batch=16, seed=G + parts)
+    got = run_int4(p, gpu, layout=layout, path=kq.PATH_MFMA, rows=parts, unroll=24)
+    check(got, ref_int4(p, layout), f"mfma T=2 G={G} {layout} P={parts}")
+
+
 def test_mfma_forced_plan_unsupported(gpu):
     p = gen.int4_problem(64, 4096, 64, seed=3)
     with pytest.raises(kq.KQError) as e:
@@ -160,6 +174,9 @@ def test_mfma_forced_plan_unsupported(gpu):
     assert e.value.status == kq.KQ_EUNSUPPORTED
     with pytest.raises(kq.KQError) as e:
         run_int4(p, gpu, path=kq.PATH_MFMA, rows=4, unroll=13)  # ring depth is 2
+    assert e.value.status == kq.KQ_EUNSUPPORTED
+    with pytest.raises(kq.KQError) as e:
+        run_int4(p, gpu, path=kq.PATH_MFMA, rows=4, unroll=22)  # T = 2 has ring depth 4
     assert e.value.status == kq.KQ_EUNSUPPORTED
 
 
