@@ -48,8 +48,7 @@ bool make_plan(uint32_t M, uint32_t K, uint32_t G, uint32_t ntok, Int4Cfg cfg, m
             const uint32_t Q = (per_cu + rounds - 1) / rounds, waves = P * Q;
             const uint32_t groups_wg = rounds * Q;
             const uint32_t nwg = (ngroups + groups_wg - 1) / groups_wg;
-            const uint32_t body = 2 * mfma::kWin;
-            const uint32_t nsteps = (rounds * J8 + body - 1) / body * body;
+            const uint32_t nsteps = rounds * J8;  // whole windows (the kernel's tail takes one or two)
             const size_t lds = mfma::lds_part(waves, T, rounds, P) + mfma::lds_wstage(waves, T);
             if (lds > kLdsMax) continue;
             // padding steps move no bytes but take issue slots

@@ -60,7 +60,7 @@
 // D register slots (ring_depth: 4 at two tiles a wave, else 2; an even slot
 // also holds its span pair's weights). Every load is unconditional: rows past the end are
 // clamped to valid addresses (results discarded), and padding steps (a part
-// padded to whole windows, the last round padded to the loop body) load out
+// padded to whole windows of 8 spans) load out
 // of the descriptors' range -- zeros, which add exactly nothing, and no
 // memory traffic. Each load is first used by the compute of its own step, so
 // the waitcnt pass sees one straight sequence and waits for exactly one slot
@@ -87,7 +87,7 @@ struct Args {
     uint32_t P, Q, J, J8;        // K parts, row-group lanes, spans per part (J8: padded to windows)
     uint32_t ngroups;            // row groups (T tiles each) in total
     uint32_t groups_wg, rounds;  // row groups per workgroup (= rounds * Q)
-    uint32_t nsteps;             // steps per wave (rounds * J8), padded to two windows
+    uint32_t nsteps;             // steps per wave (rounds * J8: whole windows)
     uint32_t part_bytes;         // LDS of the K-part reduction (the weight staging follows)
 };
 
@@ -363,7 +363,7 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
     constexpr int PER = 4 / NG;          // MFMAs per group
     constexpr uint32_t MB = SB ? 4 : 2;  // meta bytes per group (per array)
     constexpr int D = ring_depth(T);     // ring depth (steps)
-    constexpr int U = 2 * kWin;          // steps per loop body (two meta windows)
+    constexpr int U = kWin;              // steps per loop body (one meta window)
 
 
     extern __shared__ __align__(16) unsigned char smem[];
@@ -429,6 +429,8 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
     // indices after unrolling) have been kept in scratch by the compiler
     SlotE<T> ring0, ring2;
     SlotO ring1, ring3;
+    // scale/bias windows: mwb receives the next window's loads, mwa holds the
+    // current one (copied from mwb at the window's first step)
     MWin<NG, SB> mwa[T], mwb[T];
     auto slot = [&](auto k) __attribute__((always_inline)) -> auto& {
         constexpr int kk = decltype(k)::value;
@@ -436,10 +438,6 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
         else if constexpr (kk == 1) return ring1;
         else if constexpr (kk == 2) return ring2;
         else return ring3;
-    };
-    auto mwin = [&](auto b) __attribute__((always_inline)) -> MWin<NG, SB>* {
-        if constexpr (decltype(b)::value == 0) return mwa;
-        else return mwb;
     };
     auto issue = [&](auto& e, Cursor c, auto win) __attribute__((always_inline)) {
         const bool ok = c.round < A.rounds && c.j < A.J;
@@ -456,7 +454,7 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
             const uint32_t lspan = p * A.J + (j2 < A.J ? j2 : A.J - 1);
 #pragma unroll
             for (int i = 0; i < T; ++i)
-                load_mwin<NG, SB>(mwin(win)[i], rS, rB,
+                load_mwin<NG, SB>(mwb[i], rS, rB,
                                   mvo[i] + lspan * NG * MB + (lok ? 0u : kOOB));
         }
         if constexpr (std::is_same_v<std::decay_t<decltype(e)>, SlotE<T>>) {
@@ -476,7 +474,7 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
     Cursor ci{0, 0};
     static_for<D>([&](auto kk) __attribute__((always_inline)) {
         constexpr int k = decltype(kk)::value;
-        issue(slot(kk), ci, std::integral_constant<int, k % kWin == 0 ? (k / kWin) % 2 : -1>{});
+        issue(slot(kk), ci, std::integral_constant<int, k % kWin == 0 ? 0 : -1>{});
         ci.advance(A.J8);
         __builtin_amdgcn_sched_barrier(0);
     });
@@ -542,9 +540,13 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
     };
 
     // ---- one step: x-only sums, then per tile the group MFMAs and epilogue.
-    // RW = the step's span within its window, B = the window's buffer.
-    auto step = [&](const auto& e, Cursor c, auto rw, auto buf) __attribute__((always_inline)) {
-        constexpr int RW = decltype(rw)::value, B = decltype(buf)::value, SP = RW & 1;
+    // RW = the step's span within its window.
+    auto step = [&](const auto& e, Cursor c, auto rw) __attribute__((always_inline)) {
+        constexpr int RW = decltype(rw)::value, SP = RW & 1;
+        if constexpr (RW == 0) {
+#pragma unroll
+            for (int i = 0; i < T; ++i) mwa[i] = mwb[i];
+        }
         if constexpr (SP == 0) {  // stage the pair's weights in LDS (this wave's area)
 #pragma unroll
             for (int i = 0; i < T; ++i)
@@ -563,7 +565,7 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
 #pragma unroll
         for (int i = 0; i < T; ++i) {
             wv[i] = *reinterpret_cast<const u32x4*>(wst + i * 2048 + rdo[SP]);
-            m[i] = meta_at<NG, SB, RW>(mwin(std::integral_constant<int, B>{})[i], ba[RW / 2]);
+            m[i] = meta_at<NG, SB, RW>(mwa[i], ba[RW / 2]);
         }
         f32x4 sums{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -601,31 +603,27 @@ __global__ __launch_bounds__(64 * WAVES) void int4_mfma(Args A) {
         if (c.round < A.rounds && c.j == A.J8 - 1) finish(c.round);
     };
 
-    // ---- main loop: U steps per body (two meta windows, so every buffer
-    // index is a constant), loads D steps ahead; then the last U steps
+    // ---- main loop: one meta window per body (every buffer index is a
+    // constant), loads D steps ahead; then the last window
     Cursor cc{0, 0};
     uint32_t ns = 0;
     for (; ns + U < A.nsteps; ns += U) {
         static_for<U>([&](auto dd) __attribute__((always_inline)) {
             constexpr int d = decltype(dd)::value;
-            step(slot(std::integral_constant<int, d % D>{}), cc, std::integral_constant<int, d % kWin>{},
-                 std::integral_constant<int, d / kWin>{});
+            step(slot(std::integral_constant<int, d % D>{}), cc, std::integral_constant<int, d>{});
             cc.advance(A.J8);
             constexpr int nx = d + D;  // the step issued now, relative to ns
             issue(slot(std::integral_constant<int, d % D>{}), ci,
-                  std::integral_constant<int, nx % kWin == 0 ? (nx / kWin) % 2 : -1>{});
+                  std::integral_constant<int, nx % kWin == 0 ? 0 : -1>{});
             ci.advance(A.J8);
         });
     }
     static_for<U>([&](auto dd) __attribute__((always_inline)) {
         constexpr int d = decltype(dd)::value;
-        step(slot(std::integral_constant<int, d % D>{}), cc, std::integral_constant<int, d % kWin>{},
-             std::integral_constant<int, d / kWin>{});
+        step(slot(std::integral_constant<int, d % D>{}), cc, std::integral_constant<int, d>{});
         cc.advance(A.J8);
         if constexpr (d + D < U) {
-            constexpr int nx = d + D;
-            issue(slot(std::integral_constant<int, d % D>{}), ci,
-                  std::integral_constant<int, nx % kWin == 0 ? (nx / kWin) % 2 : -1>{});
+            issue(slot(std::integral_constant<int, d % D>{}), ci, std::integral_constant<int, -1>{});
             ci.advance(A.J8);
         }
     });
