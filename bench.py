@@ -468,13 +468,16 @@ def bench_vq(torch, kq, dev, args, timer, res):
 
 
 def bench_skinny(torch, kq, dev, args, timer, res):
-    """Both config-2 shapes at each of --skinny-batches tokens through the
-    vector path, the matrix cores and AUTO's choice, each a HIP graph over 8
-    weight copies (940 MB per shape, so every byte comes from HBM)."""
+    """Each of --skinny-shapes (default: both config-2 shapes) at each of
+    --skinny-batches tokens through the vector path, the matrix cores and
+    AUTO's choice, each a HIP graph over enough weight copies (8 for the
+    config-2 shapes, at most 256) that ~940 MB of weights stream per replay,
+    so every byte comes from HBM."""
     out = {}
-    ncopy = 8
     batches = [int(b) for b in args.skinny_batches.split(",")]
-    for M, K in ((28672, 8192), (8192, 28672)):
+    shapes = [tuple(int(v) for v in sh.split("x")) for sh in args.skinny_shapes.split(",")]
+    for M, K in shapes:
+        ncopy = max(8, min(256, int(940e6 // (M * K // 2))))
         layers = make_int4_layers(torch, dev, ncopy, [("w", M, K)], seed=M)
         for batch in batches:
             x = torch.randn((batch, K), device=dev).half()
@@ -597,6 +600,8 @@ def main():
     ap.add_argument("--sections", default="step,ceiling,roofline,moe,vq,skinny,cpu")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skinny-batches", default="1,2,3,4,8,16")
+    ap.add_argument("--skinny-shapes", default="28672x8192,8192x28672",
+                    help="MxK list for the skinny section")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "

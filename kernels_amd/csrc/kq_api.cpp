@@ -67,7 +67,10 @@ kq_status run_int4(const uint32_t* W, const void* S, const void* B, kq_dtype sb_
     // (int4_valu_cost), a matrix-core pass all of them at ~1.2 (29.3-30.3 us
     // against 24.9 us at 28672 x 8192; 64-byte row pieces per load instead of
     // 1 KiB rows). Measured: the vector path wins at 1-2 tokens, the matrix
-    // cores from 3.
+    // cores from 3 -- where the weights are large. A matrix-core pass takes
+    // at least ~9 us (each wave's serial steps), so small matrices stay on the
+    // vector path longer: both durations are modelled too (1024x4096: vector
+    // up to 8 tokens, 4.1-9.1 against 9.2-9.9 us; 4096x4096 up to 4).
     if (path == KQ_PATH_AUTO) {
         if (!mfma_ok) {
             path = KQ_PATH_VALU;
@@ -76,7 +79,9 @@ kq_status run_int4(const uint32_t* W, const void* S, const void* B, kq_dtype sb_
         } else {
             const uint32_t tpp = kq::int4_mfma_tokens_per_pass(M, K, G, batch, mcfg);
             const uint32_t mp = tpp ? (batch + tpp - 1) / tpp : 1000;
-            path = 120 * mp < kq::int4_valu_cost(M, K, batch) ? KQ_PATH_MFMA : KQ_PATH_VALU;
+            const bool fewer_passes = 120 * mp < kq::int4_valu_cost(M, K, batch);
+            const bool faster = mp * kq::int4_mfma_us(M, K, G, batch, mcfg) < kq::int4_valu_us(M, K, G, batch);
+            path = fewer_passes && faster ? KQ_PATH_MFMA : KQ_PATH_VALU;
         }
     }
     if (path == KQ_PATH_VALU) {

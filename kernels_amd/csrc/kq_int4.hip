@@ -479,6 +479,13 @@ uint32_t int4_valu_cost(uint32_t M, uint32_t K, uint32_t batch) {
     return cost;
 }
 
+// A batch-1 pass streams at ~5.3 TB/s after ~3 us of launch, ramp and tail
+// (fitted: 1024x4096 .. 28672x8192 measured at 2-4 tokens, within ~15%).
+double int4_valu_us(uint32_t M, uint32_t K, uint32_t G, uint32_t batch) {
+    const double bytes = (double)M * K / 2 + (double)M * (K / G) * 4;
+    return int4_valu_cost(M, K, batch) / 100.0 * (3.0 + bytes / 5.3e6);
+}
+
 size_t int4_valu_lds_bytes(uint32_t K, uint32_t batch) {
     const uint32_t nchp = ((K >> 5) + 63) / 64 * 64;
     return vlds_x(batch < kMaxNB ? batch : kMaxNB, nchp);

@@ -48,7 +48,7 @@ bool make_plan(uint32_t M, uint32_t K, uint32_t G, uint32_t ntok, Int4Cfg cfg, m
             const uint32_t Q = (per_cu + rounds - 1) / rounds, waves = P * Q;
             const uint32_t groups_wg = rounds * Q;
             const uint32_t nwg = (ngroups + groups_wg - 1) / groups_wg;
-            const uint32_t nsteps = rounds * J8;  // whole windows (the kernel's tail takes one or two)
+            const uint32_t nsteps = rounds * J8;  // whole windows (the loop body is one)
             const size_t lds = mfma::lds_part(waves, T, rounds, P) + mfma::lds_wstage(waves, T);
             if (lds > kLdsMax) continue;
             // padding steps move no bytes but take issue slots
@@ -72,6 +72,18 @@ bool make_plan(uint32_t M, uint32_t K, uint32_t G, uint32_t ntok, Int4Cfg cfg, m
 uint32_t int4_mfma_tokens_per_pass(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg) {
     mfma::Plan pl;
     return int4_mfma_supported(M, K, G, batch, cfg) && make_plan(M, K, G, batch, cfg, pl) ? batch : 0;
+}
+
+// The pass is bound by each wave's serial steps (dequant, MFMA chains,
+// epilogue), not by HBM at these sizes: ~0.42 us per (step x tile) at 8 waves
+// a CU, plus ~3.3 us of launch and ramp, ~2% more per token above 4 (fitted:
+// 1024x4096 .. 8192x28672 at 3-16 tokens).
+double int4_mfma_us(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg) {
+    mfma::Plan pl;
+    if (!make_plan(M, K, G, batch, cfg, pl)) return 1e30;
+    const uint32_t cu = cu_count();
+    const double work = (double)pl.nsteps * pl.T * (pl.waves / 8.0) * ((pl.nwg + cu - 1) / cu);
+    return 3.3 + 0.42 * work * (1.0 + 0.02 * ((double)batch - 4.0));
 }
 
 Int4Cfg int4_mfma_default(uint32_t, uint32_t, uint32_t) { return Int4Cfg{0, 0}; }

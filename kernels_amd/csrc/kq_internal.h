@@ -22,6 +22,8 @@ Int4Cfg int4_valu_default(uint32_t M, uint32_t K, uint32_t batch);
 size_t int4_valu_lds_bytes(uint32_t K, uint32_t batch);
 // `batch` tokens on the vector path in batch-1-pass units x 100 (AUTO's crossover).
 uint32_t int4_valu_cost(uint32_t M, uint32_t K, uint32_t batch);
+// Modelled duration (us) of `batch` tokens on the vector path (AUTO's crossover).
+double int4_valu_us(uint32_t M, uint32_t K, uint32_t G, uint32_t batch);
 
 // gsel (device pointer, may be null): the kernel reads the matrix index
 // gsel[0] and moves W, S and B by gsel[0] * gstride bytes -- one matrix of a
@@ -40,6 +42,8 @@ bool int4_mfma_supported(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int
 Int4Cfg int4_mfma_default(uint32_t M, uint32_t K, uint32_t batch);
 // Tokens one matrix-core pass takes (all of them; 0: the shape is not supported).
 uint32_t int4_mfma_tokens_per_pass(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg);
+// Modelled duration (us) of one matrix-core pass (AUTO's crossover).
+double int4_mfma_us(uint32_t M, uint32_t K, uint32_t G, uint32_t batch, Int4Cfg cfg);
 
 // Debug scalar path: one thread per (row, token), plain chunk loop (v0).
 hipError_t launch_int4_scalar(const uint32_t* W, const uint16_t* S, const uint16_t* B,
