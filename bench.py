@@ -139,7 +139,44 @@ def bench_int4_step(torch, kq, dev, args, timer, res):
         per[f"{M}x{K}"] = dict(us=round(us, 3), gbs=round(b / us / 1e3, 1),
                                frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4), bytes=b)
     res["per_shape"] = per
-    del layers, g
+    del g
+
+    # The same weights with the projections that share an input stored as one
+    # matrix, as inference engines keep them: q, k and v rows stacked
+    # (6144x4096), gate and up rows stacked (28672x4096); o and down as they
+    # are. 4 launches a layer instead of 7, the same weight and metadata
+    # bytes (x is read once per launch). Reported beside the 7-GEMV step.
+    fused = []
+    for L in layers:
+        F = {}
+        for name, parts in (("qkv", ("q", "k", "v")), ("gateup", ("gate", "up"))):
+            W = torch.cat([L[p][0] for p in parts])
+            SB = torch.cat([L[p][1] for p in parts])
+            F[name] = (W, SB, W.shape[0], L[parts[0]][3])
+        F["o"], F["down"] = L["o"], L["down"]
+        fused.append(F)
+    del layers
+    torch.cuda.empty_cache()
+    yf = {M: torch.empty((1, M), dtype=torch.float16, device=dev) for M in (4096, 6144, 28672)}
+    order = ("qkv", "o", "gateup", "down")
+    fused_bytes = sum(int4_bytes(fused[0][n][2], fused[0][n][3]) for n in order) * N_LAYERS
+
+    def fstep():
+        for F in fused:
+            for name in order:
+                W, SB, M, K = F[name]
+                kq.int4_gemv(W, SB, x[K], yf[M], kq.GemvParams(M, K, G))
+
+    gf = graph_of(torch, fstep)
+    for _ in range(args.warmup):
+        gf.replay()
+    fms = timer.run(lambda i: gf.replay(), args.steps, 0)
+    res["step_fused"] = dict(ms=round(fms, 4), launches=len(order) * N_LAYERS, bytes=fused_bytes,
+                             gbs=round(fused_bytes / fms / 1e6, 1),
+                             frac=round(fused_bytes / fms / 1e6 / HBM_PEAK_GBS, 4),
+                             shapes="6144x4096 (q|k|v), 4096x4096 (o), 28672x4096 (gate|up), "
+                                    "4096x14336 (down)")
+    del fused, gf
     torch.cuda.empty_cache()
 
 
@@ -623,7 +660,7 @@ def main():
     if "step" in sections:
         log("[bench] int4 decode step (Llama-3-8B, 32 layers)")
         bench_int4_step(torch, kq, dev, args, timer, res)
-        log(f"[bench] step {res['step']}")
+        log(f"[bench] step {res['step']} fused projections {res.get('step_fused')}")
     if "ceiling" in sections:
         log("[bench] stream-read ceiling")
         bench_ceiling(torch, kq, dev, timer, res)
@@ -676,6 +713,7 @@ def main():
         "roofline": res.get("roofline"),
         "cpu_baseline": cpu,
         "per_shape": res.get("per_shape"),
+        "step_fused_projections": res.get("step_fused"),
         "ceiling": res.get("ceiling"),
         "ceiling_1GiB": res.get("ceiling_1GiB"),
         "ceiling_sweep": res.get("ceiling_sweep"),
