@@ -440,6 +440,22 @@ def bench_moe(torch, kq, dev, args, timer, res, n_layers=36):
                                     frac=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
         del g
         if batch == 1:
+            # the other launch structures of the same block, same layers:
+            # one launch (KQ_MOE_PATH_ONE) and the reference's atomic sum(h)
+            # form (KQ_MOE_PATH_ATOMIC); skipped where the library refuses one
+            for pname, path in (("one_launch", kq.MOE_PATH_ONE), ("atomic", kq.MOE_PATH_ATOMIC)):
+                def pstep(path=path):
+                    for l in range(n_layers):
+                        kq.moe_block(pools[l], d, Rs[l], xs[l], idx[l], wgt[l], H, Y, ws, nws,
+                                     batch=batch, path=path)
+                try:
+                    g = graph_of(torch, pstep)
+                except kq.KQError as e:
+                    out["batch1"][pname] = dict(skipped=str(e))
+                    continue
+                pms = timer.run(lambda i: g.replay(), max(5, args.steps // 4), 2)
+                del g
+                out["batch1"][pname] = dict(us_per_block=round(pms * 1e3 / n_layers, 3))
             # the same layers one operation per launch (encodeUnfused,
             # moe-fused/src/main.mm:208-284), also replayed from a graph
             nuw = kq.moe_unfused_workspace_size(d)
