@@ -1240,13 +1240,21 @@ struct PartAssign {
     uint32_t u, r0, nr, ex;  // u = 0xFFFFFFFF: no work for this workgroup
     uint64_t m0, m1;
 };
+// Inclusive wave64 prefix sum in DPP moves (no LDS round trips): shifts
+// right by 1, 2, 4 and 8 within each 16-lane row (lanes with no source add
+// 0), then each row's last lane broadcast into the next row (row_bcast:15,
+// rows 1 and 3) and lane 31 into rows 2 and 3 (row_bcast:31).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_add(uint32_t v) {
+    return v + (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
 __device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
-    const uint32_t lane = threadIdx.x & 63;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t t = __shfl_up(v, d, 64);
-        if (lane >= (uint32_t)d) v += t;
-    }
+    v = dpp_add<0x111, 0xf>(v);  // row_shr:1
+    v = dpp_add<0x112, 0xf>(v);  // row_shr:2
+    v = dpp_add<0x114, 0xf>(v);  // row_shr:4
+    v = dpp_add<0x118, 0xf>(v);  // row_shr:8
+    v = dpp_add<0x142, 0xa>(v);  // row_bcast:15
+    v = dpp_add<0x143, 0xc>(v);  // row_bcast:31
     return v;
 }
 __device__ __forceinline__ uint32_t rl(uint32_t v, uint32_t l) {
