@@ -28,6 +28,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+WARM_S = 0.2  # seconds of replays before each timed kernel section (Timer.spans)
 LLAMA = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
          ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
 N_LAYERS = 32
@@ -48,18 +49,36 @@ class Timer:
     def __init__(self, torch):
         self.torch = torch
 
-    def run(self, fn, iters, warmup):
+    def run(self, fn, iters, warmup, warm_s=0.0):
+        return self.spans(fn, iters, warmup, 1, warm_s)[0]
+
+    def spans(self, fn, iters, warmup, n, warm_s=0.0):
+        """n back-to-back timed spans of iters calls each (ms per call). The
+        warm-up repeats batches of `warmup` calls until warm_s seconds have
+        passed (one batch at least): right after large allocations and their
+        initialisation a kernel runs several percent slower for the first
+        ~10 ms of replays. The last warm-up batch and every span are enqueued
+        without a host wait in between, so the GPU never idles (and drops
+        its clock) before or between the timed spans."""
         t = self.torch
-        for i in range(warmup):
-            fn(i)
         t.cuda.synchronize()
-        e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(iters):
-            fn(warmup + i)
-        e1.record()
+        t0, k = time.perf_counter(), 0
+        while True:
+            for _ in range(warmup):
+                fn(k)
+                k += 1
+            if time.perf_counter() - t0 >= warm_s:
+                break
+            t.cuda.synchronize()
+        ev = [t.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+        ev[0].record()
+        for s in range(n):
+            for _ in range(iters):
+                fn(k)
+                k += 1
+            ev[s + 1].record()
         t.cuda.synchronize()
-        return e0.elapsed_time(e1) / iters  # ms
+        return [ev[s].elapsed_time(ev[s + 1]) / iters for s in range(n)]  # ms
 
 
 def graph_of(torch, fn):
@@ -110,6 +129,10 @@ def bench_int4_step(torch, kq, dev, args, timer, res):
     # eager (Python launch loop) for reference
     eager_ms = timer.run(lambda i: step(), 3, 1)
     g = graph_of(torch, step)
+    # settle after the 3.93 GB of allocations and their initialisation (the
+    # first ~10 ms of replays run several percent slow), then W warm-up steps,
+    # then exactly K timed steps between host synchronisations
+    timer.run(lambda i: g.replay(), 1, 1, WARM_S)
     for _ in range(args.warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -134,7 +157,7 @@ def bench_int4_step(torch, kq, dev, args, timer, res):
                 kq.int4_gemv(W, SB, x[K], y[M], kq.GemvParams(M, K, G))
         gs = graph_of(torch, one)
         reps = max(3, args.steps // 2)
-        us = timer.run(lambda i: gs.replay(), reps, 2) * 1e3 / N_LAYERS
+        us = timer.run(lambda i: gs.replay(), reps, 2, WARM_S) * 1e3 / N_LAYERS
         b = int4_bytes(M, K)
         per[f"{M}x{K}"] = dict(us=round(us, 3), gbs=round(b / us / 1e3, 1),
                                frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4), bytes=b)
@@ -261,14 +284,21 @@ def bench_roofline(torch, kq, dev, timer, res):
             W, SB, _, _ = L["down"]
             kq.int4_gemv(W, SB, x, y, kq.GemvParams(M, K, G))
     g = graph_of(torch, one)
-    reps = 20
-    us = timer.run(lambda i: g.replay(), reps, 3) * 1e3 / N_LAYERS
+    # back-to-back timed spans of 5 replays (160 launches) each, as the
+    # reference times spans of calls (int4-gemv/src/main.mm:496-521): the
+    # median span's average launch time is the figure, the fastest span is
+    # reported beside it
+    reps, spans = 5, 7
+    per = sorted(v * 1e3 / N_LAYERS
+                 for v in timer.spans(lambda i: g.replay(), reps, 5, spans, warm_s=WARM_S))
+    us = per[spans // 2]
     b = int4_bytes(M, K)
     res["roofline"] = {"bound": "hbm", "achieved": round(b / us / 1e3, 1), "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
                        "traffic": measured_traffic(), "kernel": "int4_valu (vector path), 4096x14336, batch 1",
                        "bytes_per_launch": b, "us_per_launch": round(us, 3),
-                       "launches_timed": reps * N_LAYERS}
+                       "us_per_launch_best_span": round(per[0], 3),
+                       "launches_timed": reps * spans * N_LAYERS}
     del layers
 
 
@@ -423,7 +453,7 @@ def bench_moe(torch, kq, dev, args, timer, res, n_layers=36):
                 kq.moe_block(pools[l], d, Rs[l], xs[l], idx[l], wgt[l], H, Y, ws, nws,
                              batch=batch)
         g = graph_of(torch, step)
-        ms = timer.run(lambda i: g.replay(), max(5, args.steps // 4), 2)
+        ms = timer.run(lambda i: g.replay(), max(5, args.steps // 4), 2, WARM_S)
         # bytes actually read: the distinct selected experts' 3 projections
         # + router, per layer
         ids = idx.cpu().numpy()
@@ -453,7 +483,7 @@ def bench_moe(torch, kq, dev, args, timer, res, n_layers=36):
                 except kq.KQError as e:
                     out["batch1"][pname] = dict(skipped=str(e))
                     continue
-                pms = timer.run(lambda i: g.replay(), max(5, args.steps // 4), 2)
+                pms = timer.run(lambda i: g.replay(), max(5, args.steps // 4), 2, WARM_S)
                 del g
                 out["batch1"][pname] = dict(us_per_block=round(pms * 1e3 / n_layers, 3))
             # the same layers one operation per launch (encodeUnfused,
@@ -467,7 +497,7 @@ def bench_moe(torch, kq, dev, args, timer, res, n_layers=36):
                     nl[0] = kq.moe_block_unfused(pools[l], d, Rs[l], xs[l], idx[l], wgt[l], H, Y,
                                                  uws, nuw)
             g = graph_of(torch, ustep)
-            ums = timer.run(lambda i: g.replay(), max(5, args.steps // 4), 2)
+            ums = timer.run(lambda i: g.replay(), max(5, args.steps // 4), 2, WARM_S)
             del g
             uus = ums * 1e3 / n_layers
             out["batch1"]["unfused"] = dict(launches=nl[0], us_per_block=round(uus, 3),
@@ -495,7 +525,7 @@ def bench_vq(torch, kq, dev, args, timer, res):
             for IDX, C, S in mats:
                 kq.vq_gemv(IDX, C, S, x, y, kq.VQParams(M, K, 256, K))
         g = graph_of(torch, one)
-        us = timer.run(lambda i: g.replay(), 10, 2) * 1e3 / N_LAYERS
+        us = timer.run(lambda i: g.replay(), 10, 2, WARM_S) * 1e3 / N_LAYERS
         b = M * K // 2 + 2 * M + (M // 256) * 1024 + 2 * K + 2 * M
         out[f"{M}x{K}"] = dict(us=round(us, 3), gbs=round(b / us / 1e3, 1),
                                frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4), bytes=b)
@@ -547,7 +577,7 @@ def bench_skinny(torch, kq, dev, args, timer, res):
                     row[pname] = None
                     continue
                 g = graph_of(torch, one)
-                us = timer.run(lambda i: g.replay(), 5, 1) * 1e3 / ncopy
+                us = timer.run(lambda i: g.replay(), 5, 1, WARM_S) * 1e3 / ncopy
                 b = int4_bytes(M, K, batch)
                 row[pname] = dict(us=round(us, 2), gbs=round(b / us / 1e3, 1))
                 del g
@@ -673,6 +703,10 @@ def main():
         log("[bench] clock settle (1 GiB streaming reads until the rate plateaus)")
         res["settle"] = settle_clocks(torch, kq, dev, timer)
         log(f"[bench] settle {res['settle']}")
+    if "roofline" in sections:
+        log("[bench] roofline kernel 4096x14336")
+        bench_roofline(torch, kq, dev, timer, res)
+        log(f"[bench] roofline {res['roofline']}")
     if "step" in sections:
         log("[bench] int4 decode step (Llama-3-8B, 32 layers)")
         bench_int4_step(torch, kq, dev, args, timer, res)
@@ -681,10 +715,6 @@ def main():
         log("[bench] stream-read ceiling")
         bench_ceiling(torch, kq, dev, timer, res)
         log(f"[bench] ceiling {res['ceiling']} {res['ceiling_1GiB']}")
-    if "roofline" in sections:
-        log("[bench] roofline kernel 4096x14336")
-        bench_roofline(torch, kq, dev, timer, res)
-        log(f"[bench] roofline {res['roofline']}")
     if "traffic" in sections:
         log("[bench] counter-run launches (roofline kernel + calibration copy)")
         bench_traffic(torch, kq, dev, res)
