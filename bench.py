@@ -687,8 +687,9 @@ def main():
                     help="MxK list for the skinny section")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(see DESIGN.md, 'How the path would shard'); run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (GEMV "
+              "weights would shard by output rows, MoE experts by expert); run with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
     sections = set(args.sections.split(","))
 
