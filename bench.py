@@ -9,12 +9,19 @@ the 3.93 GB of distinct weights defeat L2 and the 256 MB MALL. The step is
 captured once as a HIP graph (224 kernel launches) and replayed.
 
 `value` = algorithmic bytes per step / time (GB/s), algorithmic bytes =
-W + (scale, bias) + x + y(fp16) per GEMV. Also reported, each from its own
-timed region: per-shape GB/s, the roofline of the dominant kernel (the
-4096x14336 GEMV), the streaming-read ceiling, the gpt-oss-120b MoE block
-(36 layers x 128 experts resident, batch 1 and 8), VQ GEMV, the skinny-GEMM
-VALU/MFMA sweep, and the CPU baseline (the reference's CPU int4 path restated
-for x86, timed on this host).
+W + (scale, bias) + x + y(fp16) per GEMV. Also reported: per-shape GB/s, the
+roofline of the dominant kernel (the 4096x14336 GEMV), the gpt-oss-120b MoE
+block (36 layers x 128 experts resident, batch 1 and 8), VQ GEMV, the
+skinny-GEMM VALU/MFMA sweep, the fixed cost of a launch inside a graph, and
+the CPU baseline (the reference's CPU int4 path restated for x86, timed on
+this host).
+
+Timing protocol (the reference's, int4-gemv/src/main.mm:417-438,496-521):
+every kernel section warms all its variants, then times them round-robin
+(one span each per round, 7 rounds, median and best reported), and the
+streaming read of each kernel's own byte count -- the best launch shape of
+the reference's unroll x threads sweep at that size -- rides in the same
+rotation, so every kernel carries its "% of same-size ceiling".
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sections ...]
 """
@@ -28,7 +35,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-WARM_S = 0.2  # seconds of replays before each timed kernel section (Timer.spans)
+WARM_S = 0.2  # seconds of replays before each timed kernel section
+ROUNDS = 7  # round-robin rounds per timed section (best and median reported)
 LLAMA = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
          ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
 N_LAYERS = 32
@@ -80,6 +88,45 @@ class Timer:
         t.cuda.synchronize()
         return [ev[s].elapsed_time(ev[s + 1]) / iters for s in range(n)]  # ms
 
+    def round_robin(self, variants, rounds=ROUNDS, warm_s=WARM_S):
+        """The reference's interleaved timing (int4-gemv/src/main.mm:496-521):
+        every variant is warmed, then timed once per round, round-robin, so
+        clock and thermal drift land on all of them alike. variants: name ->
+        (fn, calls per span, launches per call). Every warm-up batch and
+        span is enqueued with no host wait before or between the spans.
+        Returns name -> {"us": median per launch, "us_best": best per
+        launch, "spans": rounds} (microseconds)."""
+        t = self.torch
+        names = list(variants)
+        t.cuda.synchronize()
+        t0 = time.perf_counter()
+        while True:
+            for nm in names:
+                fn, calls, _ = variants[nm]
+                for _ in range(calls):
+                    fn()
+            if time.perf_counter() - t0 >= warm_s:
+                break
+            t.cuda.synchronize()
+        ev = [[t.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+              for _ in range(rounds)]
+        for r in range(rounds):
+            ev[r][0].record()
+            for i, nm in enumerate(names):
+                fn, calls, _ = variants[nm]
+                for _ in range(calls):
+                    fn()
+                ev[r][i + 1].record()
+        t.cuda.synchronize()
+        out = {}
+        for i, nm in enumerate(names):
+            _, calls, launches = variants[nm]
+            per = sorted(ev[r][i].elapsed_time(ev[r][i + 1]) * 1e3 / (calls * launches)
+                         for r in range(rounds))
+            out[nm] = {"us": round(per[rounds // 2], 3), "us_best": round(per[0], 3),
+                       "spans": rounds}
+        return out
+
 
 def graph_of(torch, fn):
     """Capture fn() (a sequence of libkq launches) as a HIP graph."""
@@ -114,7 +161,7 @@ def make_int4_layers(torch, dev, n_layers, shapes, seed=1234):
     return layers
 
 
-def bench_int4_step(torch, kq, dev, args, timer, res):
+def bench_int4_step(torch, kq, dev, args, timer, ceil, res):
     layers = make_int4_layers(torch, dev, N_LAYERS, LLAMA)
     x = {K: (torch.randn((1, K), device=dev)).half() for K in (4096, 14336)}
     y = {M: torch.empty((1, M), dtype=torch.float16, device=dev) for M in (1024, 4096, 14336)}
@@ -145,8 +192,10 @@ def bench_int4_step(torch, kq, dev, args, timer, res):
     ms = e0.elapsed_time(e1) / args.steps
     res["step"] = dict(ms=ms, bytes=step_bytes, gbs=step_bytes / ms / 1e6, eager_ms=eager_ms)
 
-    # per-shape: one graph per shape over the 32 layer copies
-    per = {}
+    # per shape: one graph per shape over the 32 layer copies, timed
+    # round-robin with the streaming read of each shape's byte count over
+    # 32 buffers
+    variants, holds, shapes = {}, [], {}
     for name, M, K in LLAMA:
         if name in ("k", "o", "up"):
             continue  # same shape as v, q, gate
@@ -156,19 +205,37 @@ def bench_int4_step(torch, kq, dev, args, timer, res):
                 W, SB, _, _ = L[name]
                 kq.int4_gemv(W, SB, x[K], y[M], kq.GemvParams(M, K, G))
         gs = graph_of(torch, one)
-        reps = max(3, args.steps // 2)
-        us = timer.run(lambda i: gs.replay(), reps, 2, WARM_S) * 1e3 / N_LAYERS
+        holds.append(gs)
         b = int4_bytes(M, K)
-        per[f"{M}x{K}"] = dict(us=round(us, 3), gbs=round(b / us / 1e3, 1),
-                               frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4), bytes=b)
+        sh = f"{M}x{K}"
+        shapes[sh] = b
+        variants[sh] = (gs.replay, 5 if b > 20e6 else 10, N_LAYERS)
+        clabel = f"int4_{b / 1e6:.2f}MB"
+        if clabel not in variants:
+            cv, hold = ceil.variant(clabel, b, N_LAYERS)
+            holds.append(hold)
+            variants[clabel] = cv
+    r = timer.round_robin(variants)
+    per = {}
+    for sh, b in shapes.items():
+        k = r[sh]
+        per[sh] = dict(us=k["us"], us_best=k["us_best"], gbs=round(b / k["us"] / 1e3, 1),
+                       frac=round(b / k["us"] / 1e3 / HBM_PEAK_GBS, 4), bytes=b,
+                       **vs_ceiling(k, r[f"int4_{b / 1e6:.2f}MB"]))
+    # the step's own ceiling: its 224 reads at the per-shape ceilings
+    step_ceil_us = N_LAYERS * sum(r[f"int4_{int4_bytes(M, K) / 1e6:.2f}MB"]["us"]
+                                  for _, M, K in LLAMA)
+    res["step"]["ceiling_ms"] = round(step_ceil_us / 1e3, 4)
+    res["step"]["of_ceiling"] = round(step_ceil_us / 1e3 / ms, 4)
     res["per_shape"] = per
-    del g
+    del holds, variants
 
     # The same weights with the projections that share an input stored as one
     # matrix, as inference engines keep them: q, k and v rows stacked
     # (6144x4096), gate and up rows stacked (28672x4096); o and down as they
     # are. 4 launches a layer instead of 7, the same weight and metadata
-    # bytes (x is read once per launch). Reported beside the 7-GEMV step.
+    # bytes (x is read once per launch). Timed round-robin with the 7-GEMV
+    # step.
     fused = []
     for L in layers:
         F = {}
@@ -178,8 +245,6 @@ def bench_int4_step(torch, kq, dev, args, timer, res):
             F[name] = (W, SB, W.shape[0], L[parts[0]][3])
         F["o"], F["down"] = L["o"], L["down"]
         fused.append(F)
-    del layers
-    torch.cuda.empty_cache()
     yf = {M: torch.empty((1, M), dtype=torch.float16, device=dev) for M in (4096, 6144, 28672)}
     order = ("qkv", "o", "gateup", "down")
     fused_bytes = sum(int4_bytes(fused[0][n][2], fused[0][n][3]) for n in order) * N_LAYERS
@@ -191,15 +256,17 @@ def bench_int4_step(torch, kq, dev, args, timer, res):
                 kq.int4_gemv(W, SB, x[K], yf[M], kq.GemvParams(M, K, G))
 
     gf = graph_of(torch, fstep)
-    for _ in range(args.warmup):
-        gf.replay()
-    fms = timer.run(lambda i: gf.replay(), args.steps, 0)
-    res["step_fused"] = dict(ms=round(fms, 4), launches=len(order) * N_LAYERS, bytes=fused_bytes,
+    r = timer.round_robin({"step": (g.replay, 2, 1), "fused": (gf.replay, 2, 1)})
+    fms = r["fused"]["us"] / 1e3
+    res["step"]["round_robin_ms"] = round(r["step"]["us"] / 1e3, 4)
+    res["step"]["round_robin_ms_best"] = round(r["step"]["us_best"] / 1e3, 4)
+    res["step_fused"] = dict(ms=round(fms, 4), ms_best=round(r["fused"]["us_best"] / 1e3, 4),
+                             launches=len(order) * N_LAYERS, bytes=fused_bytes,
                              gbs=round(fused_bytes / fms / 1e6, 1),
                              frac=round(fused_bytes / fms / 1e6 / HBM_PEAK_GBS, 4),
                              shapes="6144x4096 (q|k|v), 4096x4096 (o), 28672x4096 (gate|up), "
                                     "4096x14336 (down)")
-    del fused, gf
+    del fused, gf, g, layers
     torch.cuda.empty_cache()
 
 
@@ -222,58 +289,149 @@ def settle_clocks(torch, kq, dev, timer):
     return {"rounds": rounds, "plateau_gbs": round(best, 1)}
 
 
-def bench_ceiling(torch, kq, dev, timer, res):
-    """The streaming-read ceiling as the reference measures it
-    (int4-gemv/src/main.mm:294-334): sweep unroll {1, 2, 4, 8} x quads per
-    thread {1 .. 32} (threads = quads / (qpt * unroll), rounded to 256, at
-    least 1024) and keep the best -- "the best this machine can do on a pure
-    read, or it is not a ceiling". Two sizes: the down projection's byte
-    count rotated over 32 distinct buffers in a graph (the GEMV's protocol),
-    and 1 GiB."""
-    n = int4_bytes(4096, 14336) // 16 * 16
-    bufs = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(N_LAYERS)]
-    big = 1 << 30
-    bb = torch.empty(big, dtype=torch.uint8, device=dev)
+SWEEP = [(u, q) for u in (1, 2, 4, 8) for q in (1, 2, 4, 8, 16, 32)] + [(1, 0)]
+
+
+class Ceilings:
+    """The streaming-read ceiling at each timed kernel's own byte count, as
+    the reference measures it: a sweep of unroll {1, 2, 4, 8} x quads per
+    thread {1 .. 32} (threads = quads / (qpt * unroll), rounded down to 256,
+    at least 1024), plus this library's default shape (unroll 1 over 2048 x
+    256 threads, qpt reported as 0), keeps the best -- "the best this
+    machine can do on a pure read, or it is not a ceiling"
+    (int4-gemv/src/main.mm:294-334). The chosen shape then rides in the
+    kernel's own timing rotation, over as many buffers as the kernel has
+    weight copies, so "% of ceiling" compares two numbers measured under the
+    same clock and thermal state (int4-gemv/src/main.mm:417-438)."""
+
+    def __init__(self, torch, kq, dev, timer):
+        self.torch, self.kq, self.dev, self.timer = torch, kq, dev, timer
+        self.sink = torch.zeros(4, dtype=torch.int32, device=dev)
+        self.best = {}
+
+    @staticmethod
+    def threads(nbytes, U, qpt):
+        if qpt == 0:
+            return 2048 * 256
+        thr = (nbytes // 16) // (qpt * U) // 256 * 256
+        return thr if thr >= 1024 else None
+
+    def _bufs(self, nbytes, copies):
+        return [self.torch.empty(nbytes, dtype=self.torch.uint8, device=self.dev)
+                for _ in range(copies)]
+
+    def _graph(self, bufs, nbytes, U, thr):
+        kq, sink = self.kq, self.sink
+
+        def one():
+            for b in bufs:
+                kq.stream_read(b, nbytes, sink, unroll=U, threads=thr)
+        return graph_of(self.torch, one)
+
+    @staticmethod
+    def calls(nbytes, copies):
+        """Replays per span so that a span lasts about a millisecond."""
+        est_us = copies * (1.8 + nbytes / 7.0e6)
+        return max(1, int(1000.0 / est_us))
+
+    def sweep(self, label, nbytes, copies):
+        nbytes = nbytes // 16 * 16
+        if label in self.best:
+            return self.best[label]
+        bufs = self._bufs(nbytes, copies)
+        graphs, variants = [], {}
+        for U, q in SWEEP:
+            thr = self.threads(nbytes, U, q)
+            if thr is None:
+                continue
+            g = self._graph(bufs, nbytes, U, thr)
+            graphs.append(g)
+            variants[(U, thr, q)] = (g.replay, self.calls(nbytes, copies), copies)
+        r = self.timer.round_robin(variants, rounds=3, warm_s=0.05)
+        key = min(r, key=lambda k: r[k]["us_best"])
+        self.best[label] = {"bytes": nbytes, "copies": copies, "unroll": key[0],
+                            "threads": key[1], "qpt": key[2], "us_best": r[key]["us_best"],
+                            "gbs": round(nbytes / r[key]["us_best"] / 1e3, 1),
+                            "configs": len(variants)}
+        del graphs, bufs
+        return self.best[label]
+
+    def variant(self, label, nbytes, copies):
+        """(fn, calls, launches) of the best shape at this size over its own
+        `copies` buffers, and the holder that keeps them alive."""
+        c = self.sweep(label, nbytes, copies)
+        bufs = self._bufs(c["bytes"], copies)
+        g = self._graph(bufs, c["bytes"], c["unroll"], c["threads"])
+        return (g.replay, self.calls(c["bytes"], copies), copies), (bufs, g)
+
+    def fit(self):
+        """Least-squares t = fixed + bytes / rate over the best reads of
+        every size swept (the fixed part is what one launch costs beyond
+        its bytes)."""
+        pts = [(c["bytes"], c["us_best"]) for c in self.best.values()]
+        if len(pts) < 2:
+            return None
+        n = len(pts)
+        mx = sum(b for b, _ in pts) / n
+        my = sum(t for _, t in pts) / n
+        sxx = sum((b - mx) ** 2 for b, _ in pts)
+        slope = sum((b - mx) * (t - my) for b, t in pts) / sxx
+        return {"fixed_us": round(my - slope * mx, 3), "rate_gbs": round(1e-3 / slope, 1),
+                "sizes": n}
+
+
+def rot_copies(nbytes):
+    """Buffers a rotation needs: 32 (the GEMV protocol) up to 64 MB, else
+    enough that a replay streams more than 1 GB (beyond the 256 MB MALL)."""
+    return N_LAYERS if nbytes <= 64e6 else max(2, -(-int(1.1e9) // int(nbytes)))
+
+
+def vs_ceiling(kern, ceil):
+    """A kernel's timing against the same-size read timed in its rotation."""
+    return {"ceiling_us": ceil["us"], "ceiling_us_best": ceil["us_best"],
+            "of_ceiling": round(ceil["us"] / kern["us"], 4),
+            "of_ceiling_best": round(ceil["us_best"] / kern["us_best"], 4)}
+
+
+def bench_floor(torch, kq, dev, timer, res):
+    """The fixed cost of one launch inside a HIP graph: 32 launches a replay
+    of a kernel with (almost) nothing to do -- the streaming-read kernel over
+    one 16-byte quad, so one thread loads and every other thread exits --
+    on 1, 256 and 2048 workgroups of 256 threads. Timed round-robin like
+    every other section."""
+    buf = torch.zeros(16, dtype=torch.uint8, device=dev)
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
-    sweep = []
-    best33 = best1g = None
-    # the reference's grid, plus this library's default shape (unroll 1 over
-    # 2048 x 256 threads, qpt reported as 0)
-    for U, qpt in [(u, q) for u in (1, 2, 4, 8) for q in (1, 2, 4, 8, 16, 32)] + [(1, 0)]:
-        if True:
-            row = {"unroll": U, "qpt": qpt}
-            for name, nb in (("33MB", n), ("1GiB", big)):
-                thr = (nb // 16) // (qpt * U) // 256 * 256 if qpt else 2048 * 256
-                if thr < 1024:
-                    continue
-                if name == "33MB":
-                    def one(U=U, thr=thr):
-                        for b in bufs:
-                            kq.stream_read(b, n, sink, unroll=U, threads=thr)
-                    g = graph_of(torch, one)
-                    us = min(timer.run(lambda i: g.replay(), 5, 1) for _ in range(2)) * 1e3 / N_LAYERS
-                    del g
-                else:
-                    us = min(timer.run(lambda i: kq.stream_read(bb, big, sink, unroll=U, threads=thr),
-                                       4, 1) for _ in range(2)) * 1e3
-                gbs = nb / us / 1e3
-                row[name] = {"threads": thr, "us": round(us, 3), "gbs": round(gbs, 1)}
-                cfg = {"bytes": nb, "us": round(us, 3), "gbs": round(gbs, 1), "unroll": U,
-                       "threads": thr}
-                if name == "33MB" and (best33 is None or us < best33["us"]):
-                    best33 = cfg
-                if name == "1GiB" and (best1g is None or us < best1g["us"]):
-                    best1g = cfg
-            sweep.append(row)
-    res["ceiling"] = best33
-    res["ceiling_1GiB"] = best1g
-    res["ceiling_sweep"] = sweep
-    del bufs, bb
+    graphs, variants = [], {}
+    for name, thr in (("1_workgroup", 256), ("256_workgroups", 256 * 256),
+                      ("2048_workgroups", 2048 * 256)):
+        def one(thr=thr):
+            for _ in range(N_LAYERS):
+                kq.stream_read(buf, 16, sink, unroll=1, threads=thr)
+        g = graph_of(torch, one)
+        graphs.append(g)
+        variants[name] = (g.replay, 10, N_LAYERS)
+    r = timer.round_robin(variants)
+    res["launch_floor"] = {"what": "us per launch, 32 launches of a one-quad streaming read per "
+                                   "graph replay, 10 replays a span, median and best of "
+                                   f"{ROUNDS} round-robin spans", **r}
+    del graphs
 
 
-def bench_roofline(torch, kq, dev, timer, res):
+def bench_ceiling(torch, kq, dev, timer, ceil, res):
+    """1 GiB read (the machine's streaming rate, one buffer re-read) and the
+    fit of every size swept so far."""
+    c = ceil.sweep("1GiB", 1 << 30, 1)
+    res["ceiling_1GiB"] = c
+    res["ceiling_sizes"] = {k: v for k, v in ceil.best.items()}
+    res["ceiling_fit"] = ceil.fit()
+
+
+def bench_roofline(torch, kq, dev, timer, ceil, res):
     """The dominant kernel: int4 GEMV at 4096 x 14336 (33 MB per launch),
-    launched back to back over 32 weight copies on torch's current stream."""
+    launched back to back over 32 weight copies on torch's current stream,
+    timed round-robin with the streaming read of the same 33 MB over 32
+    buffers: spans of 5 graph replays (160 launches), the median span's
+    average launch time is the figure, the fastest span beside it."""
     M, K = 4096, 14336
     layers = make_int4_layers(torch, dev, N_LAYERS, [("down", M, K)], seed=99)
     x = torch.randn((1, K), device=dev).half()
@@ -284,22 +442,18 @@ def bench_roofline(torch, kq, dev, timer, res):
             W, SB, _, _ = L["down"]
             kq.int4_gemv(W, SB, x, y, kq.GemvParams(M, K, G))
     g = graph_of(torch, one)
-    # back-to-back timed spans of 5 replays (160 launches) each, as the
-    # reference times spans of calls (int4-gemv/src/main.mm:496-521): the
-    # median span's average launch time is the figure, the fastest span is
-    # reported beside it
-    reps, spans = 5, 7
-    per = sorted(v * 1e3 / N_LAYERS
-                 for v in timer.spans(lambda i: g.replay(), reps, 5, spans, warm_s=WARM_S))
-    us = per[spans // 2]
     b = int4_bytes(M, K)
+    cv, hold = ceil.variant(f"int4_{b / 1e6:.2f}MB", b, N_LAYERS)
+    r = timer.round_robin({"gemv": (g.replay, 5, N_LAYERS), "ceiling": cv})
+    us = r["gemv"]["us"]
     res["roofline"] = {"bound": "hbm", "achieved": round(b / us / 1e3, 1), "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
                        "traffic": measured_traffic(), "kernel": "int4_valu (vector path), 4096x14336, batch 1",
-                       "bytes_per_launch": b, "us_per_launch": round(us, 3),
-                       "us_per_launch_best_span": round(per[0], 3),
-                       "launches_timed": reps * spans * N_LAYERS}
-    del layers
+                       "bytes_per_launch": b, "us_per_launch": us,
+                       "us_per_launch_best_span": r["gemv"]["us_best"],
+                       "launches_timed": 5 * ROUNDS * N_LAYERS,
+                       **vs_ceiling(r["gemv"], r["ceiling"])}
+    del layers, hold
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "int4_gemv_4096x14336_traffic.json")
@@ -429,13 +583,18 @@ def make_moe_pools(torch, dev, n_layers, d, seed=7):
     return pools
 
 
-def bench_moe(torch, kq, dev, args, timer, res, n_layers=36):
+def bench_moe(torch, kq, dev, args, timer, ceil, res, n_layers=36):
+    """The gpt-oss-120b MoE block over 36 resident layers of 128 experts,
+    one HIP graph per launch structure, timed round-robin with the streaming
+    read of the bytes actually read per block (32 buffers)."""
     d = kq.moe_default_desc()
     pools = make_moe_pools(torch, dev, n_layers, d)
     gen = torch.Generator(device=dev)
     gen.manual_seed(11)
     Rs = [(torch.randn((d.n_experts, d.hidden), device=dev, generator=gen) * 0.02).half()
           for _ in range(n_layers)]
+    per_exp = 3 * (d.hidden * d.inter // 2 + 2 * 2 * d.inter * (d.hidden // 64) + 2 * d.inter)
+    router = d.n_experts * d.hidden * 2
     out = {}
     for batch in (1, 8):
         xs = [torch.randn((batch, d.hidden), device=dev, generator=gen).half()
@@ -448,44 +607,32 @@ def bench_moe(torch, kq, dev, args, timer, res, n_layers=36):
         ws = torch.empty(nws, dtype=torch.uint8, device=dev)
         kq.moe_workspace_init(ws, nws)
 
-        def step():
+        def step(path=kq.MOE_PATH_AUTO):
             for l in range(n_layers):
                 kq.moe_block(pools[l], d, Rs[l], xs[l], idx[l], wgt[l], H, Y, ws, nws,
-                             batch=batch)
+                             batch=batch, path=path)
         g = graph_of(torch, step)
-        ms = timer.run(lambda i: g.replay(), max(5, args.steps // 4), 2, WARM_S)
         # bytes actually read: the distinct selected experts' 3 projections
         # + router, per layer
         ids = idx.cpu().numpy()
         uniq = sum(len(set(ids[l].ravel().tolist())) for l in range(n_layers))
-        per_exp = 3 * (d.hidden * d.inter // 2 + 2 * 2 * d.inter * (d.hidden // 64) + 2 * d.inter)
-        router = d.n_experts * d.hidden * 2
         b = uniq * per_exp + n_layers * router
-        us_block = ms * 1e3 / n_layers
-        out[f"batch{batch}"] = dict(us_per_block=round(us_block, 3),
-                                    us_per_token_per_block=round(us_block / batch, 3),
-                                    unique_experts_per_block=round(uniq / n_layers, 2),
-                                    bytes_per_block=int(b / n_layers),
-                                    gbs=round(b / (ms * 1e-3) / 1e9, 1),
-                                    frac=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
-        del g
+        bpb = b // n_layers
+        holds = [g]
+        variants = {"block": (g.replay, 2, n_layers)}
         if batch == 1:
             # the other launch structures of the same block, same layers:
             # one launch (KQ_MOE_PATH_ONE) and the reference's atomic sum(h)
             # form (KQ_MOE_PATH_ATOMIC); skipped where the library refuses one
+            skipped = {}
             for pname, path in (("one_launch", kq.MOE_PATH_ONE), ("atomic", kq.MOE_PATH_ATOMIC)):
-                def pstep(path=path):
-                    for l in range(n_layers):
-                        kq.moe_block(pools[l], d, Rs[l], xs[l], idx[l], wgt[l], H, Y, ws, nws,
-                                     batch=batch, path=path)
                 try:
-                    g = graph_of(torch, pstep)
+                    gp = graph_of(torch, lambda path=path: step(path))
                 except kq.KQError as e:
-                    out["batch1"][pname] = dict(skipped=str(e))
+                    skipped[pname] = str(e)
                     continue
-                pms = timer.run(lambda i: g.replay(), max(5, args.steps // 4), 2, WARM_S)
-                del g
-                out["batch1"][pname] = dict(us_per_block=round(pms * 1e3 / n_layers, 3))
+                holds.append(gp)
+                variants[pname] = (gp.replay, 2, n_layers)
             # the same layers one operation per launch (encodeUnfused,
             # moe-fused/src/main.mm:208-284), also replayed from a graph
             nuw = kq.moe_unfused_workspace_size(d)
@@ -496,21 +643,47 @@ def bench_moe(torch, kq, dev, args, timer, res, n_layers=36):
                 for l in range(n_layers):
                     nl[0] = kq.moe_block_unfused(pools[l], d, Rs[l], xs[l], idx[l], wgt[l], H, Y,
                                                  uws, nuw)
-            g = graph_of(torch, ustep)
-            ums = timer.run(lambda i: g.replay(), max(5, args.steps // 4), 2, WARM_S)
-            del g
-            uus = ums * 1e3 / n_layers
-            out["batch1"]["unfused"] = dict(launches=nl[0], us_per_block=round(uus, 3),
-                                            over_fused=round(uus / us_block, 3))
+            gu = graph_of(torch, ustep)
+            holds.append(gu)
+            variants["unfused"] = (gu.replay, 1, n_layers)
+        cv, hold = ceil.variant(f"moe_b{batch}_{bpb / 1e6:.1f}MB", bpb, rot_copies(bpb))
+        holds.append(hold)
+        variants["ceiling"] = cv
+        r = timer.round_robin(variants)
+        us_block = r["block"]["us"]
+        row = dict(us_per_block=us_block, us_per_block_best=r["block"]["us_best"],
+                   us_per_token_per_block=round(us_block / batch, 3),
+                   unique_experts_per_block=round(uniq / n_layers, 2),
+                   bytes_per_block=bpb,
+                   gbs=round(bpb / us_block / 1e3, 1),
+                   frac=round(bpb / us_block / 1e3 / HBM_PEAK_GBS, 4),
+                   **vs_ceiling(r["block"], r["ceiling"]))
+        if batch == 1:
+            for pname in ("one_launch", "atomic"):
+                if pname in r:
+                    row[pname] = dict(us_per_block=r[pname]["us"],
+                                      us_per_block_best=r[pname]["us_best"])
+                else:
+                    row[pname] = dict(skipped=skipped.get(pname))
+            row["unfused"] = dict(launches=nl[0], us_per_block=r["unfused"]["us"],
+                                  us_per_block_best=r["unfused"]["us_best"],
+                                  over_fused=round(r["unfused"]["us"] / us_block, 3))
+        out[f"batch{batch}"] = row
+        del holds, variants, g
     res["moe"] = out
     del pools
     torch.cuda.empty_cache()
 
 
-def bench_vq(torch, kq, dev, args, timer, res):
+def bench_vq(torch, kq, dev, args, timer, ceil, res):
+    """VQ GEMV at both config-3 shapes over 32 matrices each, timed
+    round-robin with the int4 GEMV at the same shapes (the reference's
+    equal-bytes comparison, vq-gemv/src/main.mm) and the streaming read of
+    each kernel's byte count."""
     out = {}
     gen = torch.Generator(device=dev)
     gen.manual_seed(5)
+    variants, holds, nbytes = {}, [], {}
     for M, K in ((14336, 4096), (4096, 14336)):
         mats = []
         for _ in range(N_LAYERS):
@@ -521,68 +694,109 @@ def bench_vq(torch, kq, dev, args, timer, res):
         x = torch.randn((1, K), device=dev).half()
         y = torch.empty((1, M), dtype=torch.float16, device=dev)
 
-        def one():
+        def one(mats=mats, x=x, y=y, M=M, K=K):
             for IDX, C, S in mats:
                 kq.vq_gemv(IDX, C, S, x, y, kq.VQParams(M, K, 256, K))
         g = graph_of(torch, one)
-        us = timer.run(lambda i: g.replay(), 10, 2, WARM_S) * 1e3 / N_LAYERS
+        layers = make_int4_layers(torch, dev, N_LAYERS, [("w", M, K)], seed=M + K)
+        yi = torch.empty((1, M), dtype=torch.float16, device=dev)
+
+        def ione(layers=layers, x=x, yi=yi, M=M, K=K):
+            for L in layers:
+                W, SB, _, _ = L["w"]
+                kq.int4_gemv(W, SB, x, yi, kq.GemvParams(M, K, G))
+        gi = graph_of(torch, ione)
+        holds += [mats, g, layers, gi]
         b = M * K // 2 + 2 * M + (M // 256) * 1024 + 2 * K + 2 * M
-        out[f"{M}x{K}"] = dict(us=round(us, 3), gbs=round(b / us / 1e3, 1),
-                               frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4), bytes=b)
-        del mats, g
+        sh = f"{M}x{K}"
+        nbytes[sh] = b
+        variants[sh] = (g.replay, 5, N_LAYERS)
+        variants[f"int4_{sh}"] = (gi.replay, 5, N_LAYERS)
+        cv, hold = ceil.variant(f"vq_{b / 1e6:.2f}MB", b, N_LAYERS)
+        holds.append(hold)
+        variants[f"ceiling_{sh}"] = cv
+    r = timer.round_robin(variants)
+    for sh, b in nbytes.items():
+        k, ki = r[sh], r[f"int4_{sh}"]
+        M, K = (int(v) for v in sh.split("x"))
+        bi = int4_bytes(M, K)
+        out[sh] = dict(us=k["us"], us_best=k["us_best"], gbs=round(b / k["us"] / 1e3, 1),
+                       frac=round(b / k["us"] / 1e3 / HBM_PEAK_GBS, 4), bytes=b,
+                       int4_us=ki["us"], int4_bytes=bi,
+                       time_per_byte_vs_int4=round((k["us"] / b) / (ki["us"] / bi), 3),
+                       **vs_ceiling(k, r[f"ceiling_{sh}"]))
+    del holds, variants
     # the quantiser that makes this format (vq-gemv/quant/pq_quantize.py:28-83)
     # from dense N(0, 0.02) weights: 14336 x 4096, reference defaults (25
     # iterations, 200000-point sample), both formats
     M, K = 14336, 4096
     W = torch.randn((M, K), device=dev, generator=gen) * 0.02
-    for name, R, G in (("cb256_rowscale", 256, K), ("reference_cb1_g32", M, 32)):
+    for name, R, Gq in (("cb256_rowscale", 256, K), ("reference_cb1_g32", M, 32)):
         nblk = (M + R - 1) // R
         IDX = torch.empty((M, K // 2), dtype=torch.uint8, device=dev)
         C = torch.empty((nblk, 256, 2), dtype=torch.float16, device=dev)
-        S = torch.empty((M, K // G), dtype=torch.float16, device=dev)
-        wsb = kq.vq_quantize_workspace_size(M, K, R, G)
+        S = torch.empty((M, K // Gq), dtype=torch.float16, device=dev)
+        wsb = kq.vq_quantize_workspace_size(M, K, R, Gq)
         ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
-        kq.vq_quantize(W, IDX, C, S, M, K, R, G, ws, wsb)
-        ms = timer.run(lambda i: kq.vq_quantize(W, IDX, C, S, M, K, R, G, ws, wsb), 3, 1)
+        kq.vq_quantize(W, IDX, C, S, M, K, R, Gq, ws, wsb)
+        ms = timer.run(lambda i: kq.vq_quantize(W, IDX, C, S, M, K, R, Gq, ws, wsb), 3, 1)
         out[f"quantize_{M}x{K}_{name}"] = dict(ms=round(ms, 3), iters=25, sample=200_000,
                                                launches=3 + 2 * 25)
     del W
     res["vq"] = out
 
 
-def bench_skinny(torch, kq, dev, args, timer, res):
+def bench_skinny(torch, kq, dev, args, timer, ceil, res):
     """Each of --skinny-shapes (default: both config-2 shapes) at each of
     --skinny-batches tokens through the vector path, the matrix cores and
     AUTO's choice, each a HIP graph over enough weight copies (8 for the
     config-2 shapes, at most 256) that ~940 MB of weights stream per replay,
-    so every byte comes from HBM."""
+    so every byte comes from HBM; every (tokens, path) of a shape is timed
+    round-robin with the streaming read of the weights' bytes over as many
+    buffers."""
     out = {}
     batches = [int(b) for b in args.skinny_batches.split(",")]
     shapes = [tuple(int(v) for v in sh.split("x")) for sh in args.skinny_shapes.split(",")]
     for M, K in shapes:
         ncopy = max(8, min(256, int(940e6 // (M * K // 2))))
         layers = make_int4_layers(torch, dev, ncopy, [("w", M, K)], seed=M)
+        variants, holds, keys = {}, [], []
         for batch in batches:
             x = torch.randn((batch, K), device=dev).half()
             y = torch.empty((batch, M), dtype=torch.float16, device=dev)
-            row = {}
             for pname, path in (("valu", kq.PATH_VALU), ("mfma", kq.PATH_MFMA), ("auto", kq.PATH_AUTO)):
-                def one(path=path):
+                def one(path=path, x=x, y=y, batch=batch):
                     for L in layers:
                         W, SB, _, _ = L["w"]
                         kq.int4_gemv(W, SB, x, y, kq.GemvParams(M, K, G), batch=batch, path=path)
                 try:
                     one()
                 except kq.KQError:
-                    row[pname] = None
+                    keys.append((batch, pname, None))
                     continue
                 g = graph_of(torch, one)
-                us = timer.run(lambda i: g.replay(), 5, 1, WARM_S) * 1e3 / ncopy
+                holds += [g, x, y]
+                variants[(batch, pname)] = (g.replay, 2, ncopy)
+                keys.append((batch, pname, True))
+        wb = int4_bytes(M, K, 0)
+        cv, hold = ceil.variant(f"skinny_{M}x{K}", wb, ncopy)
+        holds.append(hold)
+        variants["ceiling"] = cv
+        r = timer.round_robin(variants, rounds=5)
+        for batch in batches:
+            row = {}
+            for pname in ("valu", "mfma", "auto"):
+                if (batch, pname) not in r:
+                    row[pname] = None
+                    continue
+                k = r[(batch, pname)]
                 b = int4_bytes(M, K, batch)
-                row[pname] = dict(us=round(us, 2), gbs=round(b / us / 1e3, 1))
-                del g
+                row[pname] = dict(us=k["us"], us_best=k["us_best"], gbs=round(b / k["us"] / 1e3, 1),
+                                  of_ceiling=round(r["ceiling"]["us"] / k["us"], 4))
             out[f"{M}x{K}_b{batch}"] = row
-        del layers
+        out[f"{M}x{K}_ceiling"] = dict(us=r["ceiling"]["us"], us_best=r["ceiling"]["us_best"],
+                                       bytes=wb, copies=ncopy)
+        del layers, holds, variants
         torch.cuda.empty_cache()
     res["skinny"] = out
 
@@ -680,7 +894,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--sections", default="step,ceiling,roofline,moe,vq,skinny,cpu")
+    ap.add_argument("--sections", default="floor,roofline,step,moe,vq,skinny,ceiling,cpu")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skinny-batches", default="1,2,3,4,8,16")
     ap.add_argument("--skinny-shapes", default="28672x8192,8192x28672",
@@ -700,38 +914,45 @@ def main():
     timer = Timer(torch)
     res = {}
     t_start = time.time()
-    if sections & {"step", "ceiling", "roofline", "moe", "vq", "skinny"}:  # timed sections
+    timed = {"floor", "step", "ceiling", "roofline", "moe", "vq", "skinny"}
+    if sections & timed:
         log("[bench] clock settle (1 GiB streaming reads until the rate plateaus)")
         res["settle"] = settle_clocks(torch, kq, dev, timer)
         log(f"[bench] settle {res['settle']}")
+    ceil = Ceilings(torch, kq, dev, timer)
+    if "floor" in sections:
+        log("[bench] launch floor (near-empty kernel, 32 launches per graph replay)")
+        bench_floor(torch, kq, dev, timer, res)
+        log(f"[bench] floor {res['launch_floor']}")
     if "roofline" in sections:
-        log("[bench] roofline kernel 4096x14336")
-        bench_roofline(torch, kq, dev, timer, res)
+        log("[bench] roofline kernel 4096x14336 (round-robin with its same-size read)")
+        bench_roofline(torch, kq, dev, timer, ceil, res)
         log(f"[bench] roofline {res['roofline']}")
     if "step" in sections:
         log("[bench] int4 decode step (Llama-3-8B, 32 layers)")
-        bench_int4_step(torch, kq, dev, args, timer, res)
-        log(f"[bench] step {res['step']} fused projections {res.get('step_fused')}")
-    if "ceiling" in sections:
-        log("[bench] stream-read ceiling")
-        bench_ceiling(torch, kq, dev, timer, res)
-        log(f"[bench] ceiling {res['ceiling']} {res['ceiling_1GiB']}")
+        bench_int4_step(torch, kq, dev, args, timer, ceil, res)
+        log(f"[bench] step {res['step']} per shape {res['per_shape']} "
+            f"fused projections {res.get('step_fused')}")
     if "traffic" in sections:
         log("[bench] counter-run launches (roofline kernel + calibration copy)")
         bench_traffic(torch, kq, dev, res)
         log(f"[bench] traffic {res['traffic_run']}")
     if "moe" in sections:
         log("[bench] MoE block, 36 layers x 128 experts")
-        bench_moe(torch, kq, dev, args, timer, res)
+        bench_moe(torch, kq, dev, args, timer, ceil, res)
         log(f"[bench] moe {res['moe']}")
     if "vq" in sections:
         log("[bench] VQ GEMV")
-        bench_vq(torch, kq, dev, args, timer, res)
+        bench_vq(torch, kq, dev, args, timer, ceil, res)
         log(f"[bench] vq {res['vq']}")
     if "skinny" in sections:
         log("[bench] skinny GEMM sweep")
-        bench_skinny(torch, kq, dev, args, timer, res)
+        bench_skinny(torch, kq, dev, args, timer, ceil, res)
         log(f"[bench] skinny {res['skinny']}")
+    if "ceiling" in sections:
+        log("[bench] stream-read ceiling (1 GiB) and the fit over every size swept")
+        bench_ceiling(torch, kq, dev, timer, ceil, res)
+        log(f"[bench] ceiling 1GiB {res['ceiling_1GiB']} fit {res['ceiling_fit']}")
     cpu = None
     if "cpu" in sections:
         log("[bench] CPU baseline")
@@ -761,9 +982,10 @@ def main():
         "cpu_baseline": cpu,
         "per_shape": res.get("per_shape"),
         "step_fused_projections": res.get("step_fused"),
-        "ceiling": res.get("ceiling"),
+        "launch_floor": res.get("launch_floor"),
         "ceiling_1GiB": res.get("ceiling_1GiB"),
-        "ceiling_sweep": res.get("ceiling_sweep"),
+        "ceiling_sizes": res.get("ceiling_sizes"),
+        "ceiling_fit": res.get("ceiling_fit"),
         "settle": res.get("settle"),
         "moe": res.get("moe"),
         "vq": res.get("vq"),

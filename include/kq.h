@@ -226,6 +226,17 @@ void kq_moe_default_desc(kq_moe_desc* d);
 size_t kq_moe_workspace_size(const kq_moe_desc* d, uint32_t batch);
 kq_status kq_moe_workspace_init(void* ws, size_t bytes, kq_stream_t stream);
 
+/* Reads the workspace's error word into *err after the work already on
+ * `stream` (this call synchronises the stream, the one entry point that
+ * does); with `clear` non-zero a set word is reset to 0 by a kernel on
+ * `stream` before the call returns. *err != 0 means a one-launch block on
+ * this workspace gave up waiting and its outputs are invalid. ws_bytes must
+ * cover the workspace head (at least 256 bytes). No counterpart in the
+ * reference, whose Metal command buffers report a failed dispatch through
+ * their status (int4-gemv/src/main.mm:109-113). */
+kq_status kq_moe_workspace_error(void* ws, size_t ws_bytes, uint32_t* err, int clear,
+                                 kq_stream_t stream);
+
 /* Router logits (fp32 accumulation) for every token, top_k by repeated
  * argmax (strictly greater wins, so the lowest index wins ties), softmax over
  * the selected logits. idx: uint32 [batch][top_k] in descending-logit order;
@@ -282,8 +293,10 @@ kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d,
  * kq_moe_workspace_size). KQ_EUNSUPPORTED too unless batch is 1, hidden and
  * inter need the same number of 1024-element steps, and each wave's down
  * rows fit its registers (ceil(ceil(hidden / (2 x CUs)) / floor(8 / top_k))
- * <= 4, 2 when hidden > 3072). New: the reference always encodes three
- * passes.
+ * <= 4, 2 when hidden > 3072). A PATH_ONE call needs every CU to itself:
+ * it must not overlap any other work on the device, another PATH_ONE call
+ * on another stream included (kq_moe_workspace_error reads the error word
+ * a give-up sets). New: the reference always encodes three passes.
  * KQ_MOE_PATH_ATOMIC: the reference's atomic sum(h) block
  * (fused_gate_up_swiglu_at and fused_down_combine_at,
  * moe-fused/src/kernels.metal:400-487; encodeFused with atomicVar,
@@ -312,8 +325,10 @@ kq_status kq_moe_block_path(const uint8_t* pool, const kq_moe_desc* d,
  * device memory, one per GPU, held until the process ends; the call
  * allocates nothing. A (desc, batch) whose kq_moe_workspace_size exceeds
  * KQ_MOE_NOALLOC_WS_BYTES returns KQ_EWORKSPACE (gpt-oss-120b shapes fit up
- * to 16 tokens). The first call on a GPU looks the array up and zero-fills
- * it with a kernel on `stream`. Every call on one GPU shares that GPU's
+ * to 16 tokens). The first call on a GPU looks the array's address up
+ * (hipGetSymbolAddress) and enqueues nothing else: the array starts as zeros
+ * (static storage), so a first call made under stream capture records only
+ * the block's own kernels. Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (different streams, or different
  * host threads, without ordering between them) race and must not be made.
  * Otherwise the same arguments, results and launches as kq_moe_block. */

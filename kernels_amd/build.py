@@ -53,7 +53,7 @@ def _driver(name, verbose):
     """The C++ host drivers: host-only code over the C ABI, linked against
     libkq.so (found through an $ORIGIN-relative rpath) and the HIP runtime."""
     out = os.path.join(BIN_DIR, name)
-    cmd = [os.path.join(ROCM, "llvm", "bin", "clang++"), "-O2", "-std=c++17", "-Wall", "-Wextra",
+    cmd = [os.path.join(ROCM, "llvm", "bin", "clang++"), "-O2", "-std=c++20", "-Wall", "-Wextra",
            "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROOT, "include"),
            "-I", os.path.join(ROCM, "include"), os.path.join(DRV_SRC, name + ".cpp"),
            "-o", out + ".tmp", "-L", LIB_DIR, "-lkq", "-L", os.path.join(ROCM, "lib"),

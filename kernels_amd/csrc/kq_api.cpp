@@ -3,10 +3,12 @@
 // Validation happens here, on the host, before anything is enqueued: a
 // malformed shape becomes KQ_EINVAL, never an out-of-bounds kernel. Launch
 // failures become KQ_EHIP with the HIP code kept per host thread. Nothing
-// here allocates, synchronises, prints or exits (the reference harness's die()
-// -> exit(1), int4-gemv/src/main.mm:38-42, is the caller's business now).
+// here allocates, prints or exits (the reference harness's die() -> exit(1),
+// int4-gemv/src/main.mm:38-42, is the caller's business now), and nothing
+// synchronises except kq_moe_workspace_error, a read-back query.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <cstring>
 
@@ -130,16 +132,22 @@ kq_status check_ws(const kq_moe_desc* d, uint32_t batch, const void* ws, size_t 
 }  // namespace
 
 namespace kq {
+// One cached count per device index: every planner sizes its grid for the
+// device that is current on the calling thread. The cache words are atomics,
+// so threads that query the same device for the first time at once only
+// store the same value twice.
 uint32_t cu_count() {
-    static int n = 0;
-    if (n <= 0) {
-        int dev = 0, v = 0;
-        n = hipGetDevice(&dev) == hipSuccess &&
-                    hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-                    v > 0
-                ? v
-                : 256;
-    }
+    constexpr int kDevs = 64;
+    static std::atomic<int> per_dev[kDevs];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::atomic<int>* slot = dev >= 0 && dev < kDevs ? &per_dev[dev] : nullptr;
+    int n = slot ? slot->load(std::memory_order_relaxed) : 0;
+    if (n > 0) return (uint32_t)n;
+    int v = 0;
+    n = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0 ? v
+                                                                                                   : 256;
+    if (slot) slot->store(n, std::memory_order_relaxed);
     return (uint32_t)n;
 }
 }  // namespace kq
@@ -255,6 +263,27 @@ kq_status kq_moe_workspace_init(void* ws, size_t bytes, kq_stream_t stream) {
     if (!ws) return KQ_ENULL;
     if (!aligned(ws, 256)) return KQ_EALIGN;
     return hip_status(kq::launch_ws_zero(ws, bytes, reinterpret_cast<hipStream_t>(stream)));
+}
+
+// The one entry point that waits for the GPU: the word is read back after
+// the stream's earlier work.
+kq_status kq_moe_workspace_error(void* ws, size_t ws_bytes, uint32_t* err, int clear,
+                                 kq_stream_t stream) {
+    if (!ws || !err) return KQ_ENULL;
+    if (!aligned(ws, 256)) return KQ_EALIGN;
+    if (ws_bytes < 256) return KQ_EWORKSPACE;
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    uint8_t* word = reinterpret_cast<uint8_t*>(ws) + KQ_MOE_WS_ERR_OFFSET;
+    uint32_t v = 0;
+    hipError_t e = hipMemcpyAsync(&v, word, sizeof v, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e == hipSuccess && clear && v != 0) {
+        e = kq::launch_ws_zero(word, sizeof v, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+    }
+    if (e != hipSuccess) return hip_status(e);
+    *err = v;
+    return KQ_OK;
 }
 
 kq_status kq_moe_router_topk(const void* R, kq_dtype r_dtype, const void* X, kq_dtype x_dtype,

@@ -2456,14 +2456,17 @@ hipError_t launch_one(const uint8_t* pool, const kq_moe_desc& d, const void* R, 
 }
 
 // Per-device address of `scratch`, looked up once per device (with that
-// device current) at the first kq_moe_block_noalloc call on it. The zero
-// fill at set-up is a kernel on the caller's stream (graph-safe), ahead of
-// the first block that uses the array.
+// device current) at the first kq_moe_block_noalloc call on it. Nothing is
+// enqueued for the set-up: the array has static storage and no initialiser,
+// so the loader gives every GPU's copy zeros, which is what the block needs
+// (its only state carried from call to call, the router tail's completion
+// counter, returns to zero at the end of every call). A first call made
+// under stream capture therefore records only the block's own kernels.
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch[kMaxDevices] = {};
 
-hipError_t scratch_ptr(void** out, hipStream_t s) {
+hipError_t scratch_ptr(void** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -2473,7 +2476,6 @@ hipError_t scratch_ptr(void** out, hipStream_t s) {
         void* p = nullptr;
         if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return e;
         if (p == nullptr) return hipErrorInvalidSymbol;
-        if ((e = launch_ws_zero(p, KQ_MOE_NOALLOC_WS_BYTES, s)) != hipSuccess) return e;
         g_scratch[dev] = p;
     }
     *out = g_scratch[dev];
@@ -2500,7 +2502,7 @@ hipError_t launch_moe_block_noalloc(const uint8_t* pool, const kq_moe_desc& d, c
                                     uint32_t* idx, float* wgt, uint16_t* xh, uint16_t* H, void* Y,
                                     bool y_f32, hipStream_t s) {
     void* ws = nullptr;
-    const hipError_t e = scratch_ptr(&ws, s);
+    const hipError_t e = scratch_ptr(&ws);
     if (e != hipSuccess) return e;
     return launch_moe_block(pool, d, R, r_f32, X, x_f32, batch, idx, wgt, xh, H, Y, y_f32, ws, s,
                             KQ_MOE_PATH_AUTO);

@@ -26,7 +26,7 @@ EXPORTS = ("kq_status_str", "kq_last_hip_error", "kq_version", "kq_int4_gemv",
            "kq_int4_gemv_path", "kq_int4_gemv_cfg", "kq_xsum32", "kq_stream_read",
            "kq_stream_read_cfg",
            "kq_vq_gemv", "kq_moe_default_desc", "kq_moe_workspace_size",
-           "kq_moe_workspace_init", "kq_moe_router_topk", "kq_moe_gate_up_swiglu",
+           "kq_moe_workspace_init", "kq_moe_workspace_error", "kq_moe_router_topk", "kq_moe_gate_up_swiglu",
            "kq_moe_down_combine", "kq_moe_block", "kq_moe_block_path", "kq_moe_block_noalloc",
            "kq_moe_unfused_workspace_size",
            "kq_moe_block_unfused", "kq_vq_quantize_workspace_size", "kq_vq_quantize")
@@ -81,6 +81,7 @@ def lib():
         L.kq_moe_workspace_size.argtypes = [C.POINTER(MoEDesc), u32]
         L.kq_moe_workspace_size.restype = sz
         L.kq_moe_workspace_init.argtypes = [vp, sz, vp]
+        L.kq_moe_workspace_error.argtypes = [vp, sz, C.POINTER(u32), i32, vp]
         L.kq_moe_router_topk.argtypes = [vp, i32, vp, i32, u32, C.POINTER(MoEDesc), vp, vp, vp,
                                          vp, sz, vp]
         L.kq_moe_gate_up_swiglu.argtypes = [vp, C.POINTER(MoEDesc), vp, vp, vp, u32, vp, sz, vp]
@@ -259,6 +260,15 @@ def moe_workspace_size(desc, batch):
 
 def moe_workspace_init(ws, nbytes, stream=None):
     _check(lib().kq_moe_workspace_init(_ptr(ws), nbytes, _stream(stream)), "kq_moe_workspace_init")
+
+
+def moe_workspace_error(ws, nbytes, clear=False, stream=None):
+    """The workspace's error word after the stream's earlier work (synchronises
+    the stream); non-zero: a one-launch block on it gave up waiting."""
+    v = C.c_uint32(0)
+    _check(lib().kq_moe_workspace_error(_ptr(ws), nbytes, C.byref(v), int(bool(clear)),
+                                        _stream(stream)), "kq_moe_workspace_error")
+    return v.value
 
 
 def moe_router_topk(R, x, idx, wgt, desc, ws, ws_bytes, batch=1, xh=None, stream=None):

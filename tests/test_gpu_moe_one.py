@@ -16,7 +16,23 @@ pytestmark = pytest.mark.gpu
 
 
 def err_word(b):
-    return int(b.ws[kq.MOE_WS_ERR_OFFSET:kq.MOE_WS_ERR_OFFSET + 4].cpu().numpy().view(np.uint32)[0])
+    return kq.moe_workspace_error(b.ws, b.wsb)
+
+
+def test_workspace_error_query(gpu):
+    """kq_moe_workspace_error reads the word a give-up would set and clears
+    it on request; the word is set here from the host (no wait is made to
+    give up)."""
+    d = kq.moe_default_desc()
+    b = Block(gpu, d, 1)
+    assert kq.moe_workspace_error(b.ws, b.wsb) == 0
+    b.ws[kq.MOE_WS_ERR_OFFSET:kq.MOE_WS_ERR_OFFSET + 4].copy_(
+        torch.from_numpy(np.array([0x1234], np.uint32).view(np.uint8)).to(gpu))
+    assert kq.moe_workspace_error(b.ws, b.wsb) == 0x1234  # read, not cleared
+    assert kq.moe_workspace_error(b.ws, b.wsb, clear=True) == 0x1234
+    assert kq.moe_workspace_error(b.ws, b.wsb) == 0
+    with pytest.raises(kq.KQError):
+        kq.moe_workspace_error(b.ws, 64)
 
 
 def run(pool, d, Rd, Xd, b, path, xh=True):
