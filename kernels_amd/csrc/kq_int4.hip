@@ -17,7 +17,12 @@
 //     [token][word%4][chunk] (lane-consecutive chunks: conflict-free
 //     ds_read_b128) plus per-chunk (sum, offset constant), with the chunks
 //     padded to a multiple of 64 by zeros: a lane past the end of a row
-//     contributes exactly 0 and no lane tests bounds;
+//     contributes exactly 0 and no lane tests bounds. Above 8 waves only the
+//     first few waves stage (about 4 words a thread) and the others issue
+//     their weight loads at once: a CU's load path takes every wave's first
+//     loads in turn (~7 ns a 16-byte and ~4 ns a 4-byte wave load), so the
+//     fewer staging loads ahead of the weight loads, the sooner every wave's
+//     first weights arrive;
 //   * a workgroup of P*Q waves owns a contiguous range of row groups (R rows
 //     each); wave (p, q) takes K-part p (J = steps/P consecutive steps) of row
 //     groups q, q+Q, ... ("rounds"). With P = 1 a wave finishes its rows alone
@@ -50,12 +55,13 @@ struct VArgs {
     uint32_t P, Q, J;                 // K parts, row-group lanes, steps per part
     uint32_t groups_wg, ngroups;      // row groups per workgroup / in total
     uint32_t rounds, nreal, nsteps;   // rounds per workgroup; items per wave, padded to D
+    uint32_t xw;                      // waves that stage x (the first xw of the workgroup)
     const uint32_t* gsel;             // gathered form: W, S, B move by gsel[0] * gstride
     uint64_t gstride;                 // bytes (one matrix of a pool, picked on the device)
 };
 
 struct VPlan {
-    uint32_t R, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D;
+    uint32_t R, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, xw;
     size_t lds;
 };
 
@@ -137,22 +143,25 @@ __global__ __launch_bounds__(R * D >= 16 || NB >= 3 ? 512 : 1024) void int4_valu
     const rsrc_t rB = make_rsrc(bB + (size_t)row0 * metab, rows_wg * metab);
     const rsrc_t rX = make_rsrc(A.X, NB * A.K * 2);
 
-    // ---- 1. x staging loads first (vmcnt retires in order), all in one pass
-    const uint32_t xtotal = NB * nw;
+    // ---- 1. x staging loads first (vmcnt retires in order), all in one pass,
+    // by the first A.xw waves only: the other waves go straight to their
+    // ring loads, and no wave waits for another before its first weight load
+    const uint32_t xtotal = NB * nw, xthr = A.xw * 64;
+    const bool stager = wave < A.xw;  // uniform
     u32x4 sv[kXr];
     auto x_load = [&](uint32_t w0) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < kXr; ++r) {
-            if (w0 + r * nthr >= xtotal) break;  // uniform
-            const uint32_t w = w0 + r * nthr + tid;
+            if (w0 + r * xthr >= xtotal) break;  // uniform
+            const uint32_t w = w0 + r * xthr + tid;
             sv[r] = __builtin_amdgcn_raw_buffer_load_b128(rX, w < xtotal ? w * 16 : kOOB, 0, 0);
         }
     };
     auto x_store = [&](uint32_t w0) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < kXr; ++r) {
-            if (w0 + r * nthr >= xtotal) break;  // uniform
-            const uint32_t w = w0 + r * nthr + tid;
+            if (w0 + r * xthr >= xtotal) break;  // uniform
+            const uint32_t w = w0 + r * xthr + tid;
             float s, c;
             word_consts(sv[r], s, c);
             s = quad_sum(s);
@@ -165,14 +174,7 @@ __global__ __launch_bounds__(R * D >= 16 || NB >= 3 ? 512 : 1024) void int4_valu
             }
         }
     };
-    x_load(0);
-    __builtin_amdgcn_sched_barrier(0);
-    // With more than 8 waves, the later waves' staging loads would queue in
-    // the CU's load path behind the earlier waves' ring loads, and the
-    // staging barrier waits for the last of them. A barrier (no wait) puts
-    // every wave's staging loads first. Measured at 14336 x 4096 (14 waves):
-    // 8.41 -> 7.73 us; at 8 waves or fewer it costs more than it saves.
-    if (A.P * A.Q > 8) __builtin_amdgcn_s_barrier();  // uniform
+    if (stager) x_load(0);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 2. prime the ring
@@ -217,10 +219,12 @@ __global__ __launch_bounds__(R * D >= 16 || NB >= 3 ? 512 : 1024) void int4_valu
     }
 
     // ---- 3. finish the staging, zero the padding chunks
-    x_store(0);
-    for (uint32_t w0 = kXr * nthr; w0 < xtotal; w0 += kXr * nthr) {
-        x_load(w0);
-        x_store(w0);
+    if (stager) {
+        x_store(0);
+        for (uint32_t w0 = kXr * xthr; w0 < xtotal; w0 += kXr * xthr) {
+            x_load(w0);
+            x_store(w0);
+        }
     }
     const uint32_t npad = nchp - nch;
     for (uint32_t i = tid; i < NB * 5 * npad; i += nthr) {
@@ -342,6 +346,7 @@ __global__ __launch_bounds__(R * D >= 16 || NB >= 3 ? 512 : 1024) void int4_valu
 
 
 constexpr size_t kLdsMax = 160 * 1024;
+constexpr uint32_t kXwWords = 4;
 // Tokens per pass of the vector path: up to 4 (x of every token of the pass
 // in LDS, NB accumulators per row); a batch takes passes of 4, then 3, 2 or
 // 1, each reading W once. A pass whose x does not fit LDS takes 2 tokens.
@@ -410,7 +415,17 @@ bool make_vplan(uint32_t M, uint32_t K, uint32_t ntok, Int4Cfg cfg, VPlan& out) 
                 if (!found || cost < best) {
                     found = true;
                     best = cost;
-                    out = VPlan{R, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, lds};
+                    // waves that stage x: every wave up to 8; beyond that
+                    // about kXwWords 16-byte words per staging thread, and
+                    // the other waves issue their weight loads at once
+                    // (measured against every wave staging behind a barrier:
+                    // 14336 x 4096 -0.17 us, 4096 x 4096 -0.14, 4096 x 14336
+                    // -0.02; with fewer staging waves each stages too much,
+                    // with more the barrier's wait returns)
+                    const uint32_t xwords = ntok * (K >> 3);
+                    uint32_t xw = (xwords + 64 * kXwWords - 1) / (64 * kXwWords);
+                    xw = waves <= 8 ? waves : xw < 1 ? 1 : xw > waves ? waves : xw;
+                    out = VPlan{R, P, Q, J, rounds, groups_wg, nwg, nreal, nsteps, D, xw, lds};
                 }
             }
         }
@@ -533,6 +548,7 @@ hipError_t launch_int4_valu(const uint32_t* W, const uint16_t* S, const uint16_t
         a.rounds = pl.rounds;
         a.nreal = pl.nreal;
         a.nsteps = pl.nsteps;
+        a.xw = pl.xw;
         a.gsel = gsel;
         a.gstride = gstride;
         const bool bf = meta_kind == 1;
