@@ -951,6 +951,7 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     __shared__ uint32_t s_idx[kMaxSlots];
     __shared__ float s_wgt[kMaxSlots];
     __shared__ uint32_t bits[8];
+    __shared__ uint32_t s_next;  // next item of the workgroup's range to hand out
     const uint32_t K = d.hidden, IN = d.inter, TK = d.top_k;
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t half = lane >> 5, rowb = K >> 1, metab = (K >> 6) * 2;
@@ -996,6 +997,31 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     };
     Cur ci{(k0 + wave) / IN, (k0 + wave) % IN}, cc = ci, clast = ci;
     uint32_t nis = 0;  // items issued
+    // Item k of the workgroup's range -> (plan entry u, row i): a multiply by
+    // 2^32 / IN rounded up, exact here (k0 + k < 2^32 / IN) and checked once.
+    const uint32_t inv_in = 0xFFFFFFFFu / IN + 1u;
+    auto item = [&](uint32_t k) __attribute__((always_inline)) {
+        const uint32_t g = k0 + k;
+        uint32_t u = __umulhi(g, inv_in);
+        if ((u + 1) * IN <= g) ++u;
+        return Cur{u, g - u * IN};
+    };
+    // Without AT, the items past each wave's first D go out one at a time to
+    // whichever wave refills a slot first (an LDS counter): the older wave of
+    // a SIMD issues ahead of the younger, and a fixed deal (items wave,
+    // wave + 8, ...) left the younger waves ~0.5-0.8 us behind at the end.
+    // An item past the range loads through an empty descriptor (no traffic,
+    // the same load count).
+    auto issue_k = [&](StSlot<J>& e, uint32_t k) __attribute__((always_inline)) {
+        const bool ok = k < cnt;  // uniform
+        const Cur c = item(ok ? k : 0);
+        const uint32_t ex =
+            __builtin_amdgcn_readfirstlane(min(ps.expert[min(c.u, nexp - 1)], d.n_experts - 1));
+        const rsrc_t r = make_rsrc(pool + (size_t)ex * d.blob, ok ? (uint32_t)d.blob : 0u);
+        const uint32_t i = __builtin_amdgcn_readfirstlane(c.i);
+        st_issue<J>(e, r, L, i * rowb, i * metab, i * 2);
+    };
+    uint32_t sk[D];  // the item each ring slot holds (dynamic hand-out)
     auto issue = [&](StSlot<J>& e) __attribute__((always_inline)) {
         if (nis < nit) clast = ci;  // padding re-reads the last item
         const uint32_t ex =
@@ -1010,9 +1036,15 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     // loads on every path lets the compiler wait for the staging loads alone
 #pragma unroll
     for (int s = 0; s < D; ++s) {
-        issue(ring[s]);
+        if constexpr (AT) {
+            issue(ring[s]);
+        } else {
+            sk[s] = wave + s * kStWaves;
+            issue_k(ring[s], sk[s]);
+        }
         __builtin_amdgcn_sched_barrier(0);
     }
+    if (!AT && threadIdx.x == 0) s_next = D * kStWaves;
     if constexpr (SRC == 2) {
         if (blockIdx.x == 0) publish_plan(ps, s_idx, s_wgt, batch * TK, idx_out, wgt_out, plan_out);
     }
@@ -1057,6 +1089,56 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
         H[oi] = ov;
         adv(cc);
     };
+    if constexpr (!AT) {
+        // items in increasing order per wave: the first slot that holds an
+        // item past the range ends the wave's stream
+        auto step_k = [&](const StSlot<J>& e, uint32_t k) __attribute__((always_inline)) {
+            cc = item(k);
+            step(e, 0, false);
+        };
+        // The next index: an LDS atomic by lane 0 alone, with the exec mask
+        // narrowed and restored inside one asm block (a one-lane atomic
+        // written as a branch left the waitcnt pass waiting for every load at
+        // the loop head; all 64 lanes on the one address serialise in LDS).
+        // The value is read one step later, after an LDS wait, and made
+        // uniform.
+        const uint32_t next_a =
+            (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&s_next;
+        auto take = [&]() __attribute__((always_inline)) {
+            uint32_t v = 0;
+            uint64_t saved;
+            asm volatile(
+                "s_mov_b64 %1, exec\n\t"
+                "s_mov_b64 exec, 1\n\t"
+                "ds_add_rtn_u32 %0, %2, %3\n\t"
+                "s_mov_b64 exec, %1"
+                : "+v"(v), "=&s"(saved)
+                : "v"(next_a), "v"(1u)
+                : "memory");
+            return v;
+        };
+        // every step refills its slot (an item past the range moves no
+        // bytes), so the loop body has one path and each wait counts exactly
+        // the other slot's loads and the step's store
+        static_assert(D == 2, "the loop body is written for two slots");
+        auto run = [&](int s, uint32_t& pre) __attribute__((always_inline)) {
+            step_k(ring[s], sk[s]);
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            sk[s] = __builtin_amdgcn_readfirstlane(pre);
+            issue_k(ring[s], sk[s]);
+            __builtin_amdgcn_sched_barrier(0);
+            pre = take();
+        };
+        uint32_t pre = take();
+        for (;;) {
+            if (sk[0] >= cnt) break;  // uniform
+            run(0, pre);
+            if (sk[1] >= cnt) break;
+            run(1, pre);
+        }
+        return;
+    }
     const uint32_t nsteps = (nit + D - 1) / D * D;
     uint32_t it = 0;
     for (; it + D < nsteps; it += D) {
