@@ -56,6 +56,7 @@ struct VArgs {
     uint32_t groups_wg, ngroups;      // row groups per workgroup / in total
     uint32_t rounds, nreal, nsteps;   // rounds per workgroup; items per wave, padded to D
     uint32_t xw;                      // waves that stage x (the first xw of the workgroup)
+    uint32_t pinv;                    // ceil(2^16 / P): wave / P as a multiply (exact below 16 waves)
     const uint32_t* gsel;             // gathered form: W, S, B move by gsel[0] * gstride
     uint64_t gstride;                 // bytes (one matrix of a pool, picked on the device)
 };
@@ -119,9 +120,8 @@ __global__ __launch_bounds__(R * D >= 16 || NB >= 3 ? 512 : 1024) void int4_valu
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
     const uint32_t lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t p = wave % A.P, q = wave / A.P;
+    const uint32_t q = (wave * A.pinv) >> 16, p = wave - q * A.P;
     const uint32_t g0 = blockIdx.x * A.groups_wg;
-    const uint32_t last_group = A.ngroups - 1, last_row = A.M - 1;
 
     // Descriptors based at this workgroup's first row: every offset is small,
     // and the range checks turn the lanes past a partial last step into
@@ -192,14 +192,15 @@ __global__ __launch_bounds__(R * D >= 16 || NB >= 3 ? 512 : 1024) void int4_valu
             c.round = A.rounds - 1;
             c.j = A.J - 1;
         }
-        const uint32_t grp = min(g0 + c.round * A.Q + q, last_group);
-        const uint32_t s = __builtin_amdgcn_readfirstlane(p * A.J + c.j);
+        // row rr of the workgroup: past its last row (the last workgroup's
+        // unused row groups) every load is out of range -- zeros, no bytes
+        const uint32_t s = p * A.J + c.j;
         const bool last = s == nstep - 1;
         const uint32_t vw = pad ? kOOB : last ? vw_last : vw_full;
         const uint32_t vm = pad ? kOOB : last ? vm_last : vm_full;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t rr = __builtin_amdgcn_readfirstlane(min(grp * R + r, last_row) - row0);
+            const uint32_t rr = (c.round * A.Q + q) * R + r;
             e.w[r] = __builtin_amdgcn_raw_buffer_load_b128(rW, vw, rr * rowb + s * 1024, kNT);
             const uint32_t mo = rr * metab + (s * (64u >> A.cshift)) * MB;
             if constexpr (SB) {
@@ -549,6 +550,7 @@ hipError_t launch_int4_valu(const uint32_t* W, const uint16_t* S, const uint16_t
         a.nreal = pl.nreal;
         a.nsteps = pl.nsteps;
         a.xw = pl.xw;
+        a.pinv = (65536u + pl.P - 1) / pl.P;
         a.gsel = gsel;
         a.gstride = gstride;
         const bool bf = meta_kind == 1;
