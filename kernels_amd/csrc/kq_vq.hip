@@ -48,6 +48,7 @@ struct QArgs {
     uint32_t cb_first_div;  // rows of a workgroup span at most this many codebooks
     uint32_t rpc_shift;     // log2(rows per codebook) if a power of 2; 31: one codebook
                             // for all rows; 32: divide
+    uint32_t pinv;          // ceil(2^16 / P): wave / P as a multiply (exact below 16 waves)
 };
 
 struct QPlan {
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
     const uint32_t lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t p = wave % A.P, q = wave / A.P;
+    const uint32_t q = (wave * A.pinv) >> 16, p = wave - q * A.P;
     const uint32_t g0 = blockIdx.x * A.groups_wg;
     const uint32_t last_group = A.ngroups - 1, last_row = A.M - 1;
     const uint32_t row0 = g0 * R;
@@ -196,19 +197,22 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
         return per_row ? 0u : A.cshift <= 6 ? s * (64u >> A.cshift) : s >> (A.cshift - 6);
     };
     QSlot<R> ring[D];
+    // padding items (the ring depth past the wave's items) and rows past the
+    // workgroup's last load out of range: zeros, no bytes
     auto issue = [&](QSlot<R>& e, Cursor c) __attribute__((always_inline)) {
-        if (c.round >= A.rounds) {  // padding item: re-read the last real one
+        const bool pad = c.round >= A.rounds;  // uniform
+        if (pad) {
             c.round = A.rounds - 1;
             c.j = A.J - 1;
         }
-        const uint32_t grp = min(g0 + c.round * A.Q + q, last_group);
-        const uint32_t s = __builtin_amdgcn_readfirstlane(p * A.J + c.j);
+        const uint32_t s = p * A.J + c.j;
         const bool last = s == nstep - 1;
-        const uint32_t vi = last ? vi_last : vi_full, vs = last ? vs_last : vs_full;
+        const uint32_t vi = pad ? kOOB : last ? vi_last : vi_full;
+        const uint32_t vs = pad ? kOOB : last ? vs_last : vs_full;
         const uint32_t so = scale_step(s) * 2;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t rr = __builtin_amdgcn_readfirstlane(min(grp * R + r, last_row) - row0);
+            const uint32_t rr = (c.round * A.Q + q) * R + r;
             e.idx[r] = __builtin_amdgcn_raw_buffer_load_b128(rI, vi, rr * rowb + s * 1024, kNT);
             e.sc[r] = __builtin_amdgcn_raw_buffer_load_b16(rS, vs, rr * srowb + so, 0);
         }
@@ -520,6 +524,7 @@ hipError_t launch_vq(const uint8_t* IDX, const uint16_t* C, const uint16_t* S, c
         a.rounds = pl.rounds;
         a.nreal = pl.nreal;
         a.nsteps = pl.nsteps;
+        a.pinv = (65536u + pl.P - 1) / pl.P;
         a.cb_first_div = pl.ncb;
         a.rpc_shift = rows_per_cb >= M ? 31u : 32u;
         if (rows_per_cb < M && (rows_per_cb & (rows_per_cb - 1)) == 0) {
