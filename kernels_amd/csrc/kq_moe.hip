@@ -1058,10 +1058,12 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     // One store per step, by every lane: lane j < the item's slot count writes
     // slot j's h, the other lanes repeat the last slot's write. A fixed store
     // count keeps the next ring wait from also waiting for this step's store.
-    // Steps of the main loop are never padding; only the tail checks.
-    auto step = [&](const StSlot<J>& e, uint32_t it, bool tail) __attribute__((always_inline)) {
+    // Steps of the main loop are never padding; only the tail checks. `mid`
+    // runs between the step's plan reads and its first use of the weights.
+    auto step = [&](const StSlot<J>& e, uint32_t it, bool tail, auto&& mid) __attribute__((always_inline)) {
         if (tail && it >= nit) return;  // padding (uniform)
         uint64_t m0 = ps.mask[cc.u][0], m1 = ps.mask[cc.u][1];
+        mid();
         StDq<J> q;
         st_dequant<J>(e, kc, q);
         const float bg = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 0));
@@ -1092,50 +1094,58 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     if constexpr (!AT) {
         // items in increasing order per wave: the first slot that holds an
         // item past the range ends the wave's stream
-        auto step_k = [&](const StSlot<J>& e, uint32_t k) __attribute__((always_inline)) {
+        auto step_k = [&](const StSlot<J>& e, uint32_t k, auto&& mid) __attribute__((always_inline)) {
             cc = item(k);
-            step(e, 0, false);
+            step(e, 0, false, mid);
         };
         // The next index: an LDS atomic by lane 0 alone, with the exec mask
         // narrowed and restored inside one asm block (a one-lane atomic
         // written as a branch left the waitcnt pass waiting for every load at
         // the loop head; all 64 lanes on the one address serialise in LDS).
-        // The value is read one step later, after an LDS wait, and made
-        // uniform.
+        // The same block waits for the return (the compiler does not see
+        // that wait, so a return left in flight in a register past the asm
+        // could be copied before it arrives); lane 0's value is then made
+        // uniform outside it (an asm with a VGPR output counts as divergent).
+        // Each step draws after its plan reads, before it waits for its
+        // weights (far longer than an LDS atomic), and refills its slot with
+        // the drawn item.
         const uint32_t next_a =
             (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&s_next;
-        auto take = [&]() __attribute__((always_inline)) {
-            uint32_t v = 0;
+        auto draw = [&]() __attribute__((always_inline)) {
+            uint32_t v;
             uint64_t saved;
             asm volatile(
                 "s_mov_b64 %1, exec\n\t"
                 "s_mov_b64 exec, 1\n\t"
                 "ds_add_rtn_u32 %0, %2, %3\n\t"
-                "s_mov_b64 exec, %1"
-                : "+v"(v), "=&s"(saved)
+                "s_mov_b64 exec, %1\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(v), "=&s"(saved)
                 : "v"(next_a), "v"(1u)
                 : "memory");
-            return v;
+            return __builtin_amdgcn_readfirstlane(v);
         };
         // every step refills its slot (an item past the range moves no
         // bytes), so the loop body has one path and each wait counts exactly
         // the other slot's loads and the step's store
         static_assert(D == 2, "the loop body is written for two slots");
-        auto run = [&](int s, uint32_t& pre) __attribute__((always_inline)) {
-            step_k(ring[s], sk[s]);
+        auto run = [&](int s) __attribute__((always_inline)) {
+            uint32_t nk = 0;
+            step_k(ring[s], sk[s], [&]() __attribute__((always_inline)) {
+                __builtin_amdgcn_sched_barrier(0);
+                nk = draw();
+                __builtin_amdgcn_sched_barrier(0);
+            });
             __builtin_amdgcn_sched_barrier(0);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            sk[s] = __builtin_amdgcn_readfirstlane(pre);
+            sk[s] = nk;
             issue_k(ring[s], sk[s]);
             __builtin_amdgcn_sched_barrier(0);
-            pre = take();
         };
-        uint32_t pre = take();
         for (;;) {
             if (sk[0] >= cnt) break;  // uniform
-            run(0, pre);
+            run(0);
             if (sk[1] >= cnt) break;
-            run(1, pre);
+            run(1);
         }
         return;
     }
@@ -1144,12 +1154,12 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     for (; it + D < nsteps; it += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
-            step(ring[s], it + s, false);
+            step(ring[s], it + s, false, [] {});
             issue(ring[s]);
         }
     }
 #pragma unroll
-    for (int s = 0; s < D; ++s) step(ring[s], it + s, true);
+    for (int s = 0; s < D; ++s) step(ring[s], it + s, true, [] {});
     if constexpr (AT) {  // every wave's LDS sums done; waves without items (wave >= cnt) have left
         __syncthreads();
         const uint32_t nact = 64 * min(cnt, (uint32_t)kStWaves);
