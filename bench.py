@@ -215,13 +215,16 @@ def bench_int4_step(torch, kq, dev, args, timer, ceil, res):
             cv, hold = ceil.variant(clabel, b, N_LAYERS)
             holds.append(hold)
             variants[clabel] = cv
+        cv, hold = ceil.variant_out(clabel, b, N_LAYERS, M)
+        holds.append(hold)
+        variants[f"out_{sh}"] = cv
     r = timer.round_robin(variants)
     per = {}
     for sh, b in shapes.items():
         k = r[sh]
         per[sh] = dict(us=k["us"], us_best=k["us_best"], gbs=round(b / k["us"] / 1e3, 1),
                        frac=round(b / k["us"] / 1e3 / HBM_PEAK_GBS, 4), bytes=b,
-                       **vs_ceiling(k, r[f"int4_{b / 1e6:.2f}MB"]))
+                       **vs_ceiling(k, r[f"int4_{b / 1e6:.2f}MB"], r[f"out_{sh}"]))
     # the step's own ceiling: its 224 reads at the per-shape ceilings
     step_ceil_us = N_LAYERS * sum(r[f"int4_{int4_bytes(M, K) / 1e6:.2f}MB"]["us"]
                                   for _, M, K in LLAMA)
@@ -320,12 +323,15 @@ class Ceilings:
         return [self.torch.empty(nbytes, dtype=self.torch.uint8, device=self.dev)
                 for _ in range(copies)]
 
-    def _graph(self, bufs, nbytes, U, thr):
+    def _graph(self, bufs, nbytes, U, thr, out=None, nout=0):
         kq, sink = self.kq, self.sink
 
         def one():
             for b in bufs:
-                kq.stream_read(b, nbytes, sink, unroll=U, threads=thr)
+                if out is None:
+                    kq.stream_read(b, nbytes, sink, unroll=U, threads=thr)
+                else:
+                    kq.stream_read_out(b, nbytes, out, nout, U, thr)
         return graph_of(self.torch, one)
 
     @staticmethod
@@ -364,6 +370,19 @@ class Ceilings:
         g = self._graph(bufs, c["bytes"], c["unroll"], c["threads"])
         return (g.replay, self.calls(c["bytes"], copies), copies), (bufs, g)
 
+    def variant_out(self, label, nbytes, copies, out_elems):
+        """The same best read shape, then out_elems 2-byte values stored
+        across the grid (kq_stream_read_out): the ceiling of a kernel that
+        must also store its y. A launch that stores from every XCD pays for
+        the write-back of each XCD's dirty L2 lines at its end (measured:
+        +0.37-0.47 us at 2.4-33 MB; +0.26-0.31 us even with every store
+        issued before the reads; plain stores cheaper than sc0, sc1 or nt)."""
+        c = self.sweep(label, nbytes, copies)
+        bufs = self._bufs(c["bytes"], copies)
+        out = self.torch.empty(out_elems, dtype=self.torch.int16, device=self.dev)
+        g = self._graph(bufs, c["bytes"], c["unroll"], c["threads"], out, out_elems)
+        return (g.replay, self.calls(c["bytes"], copies), copies), (bufs, out, g)
+
     def fit(self):
         """Least-squares t = fixed + bytes / rate over the best reads of
         every size swept (the fixed part is what one launch costs beyond
@@ -386,11 +405,17 @@ def rot_copies(nbytes):
     return N_LAYERS if nbytes <= 64e6 else max(2, -(-int(1.1e9) // int(nbytes)))
 
 
-def vs_ceiling(kern, ceil):
-    """A kernel's timing against the same-size read timed in its rotation."""
-    return {"ceiling_us": ceil["us"], "ceiling_us_best": ceil["us_best"],
-            "of_ceiling": round(ceil["us"] / kern["us"], 4),
-            "of_ceiling_best": round(ceil["us_best"] / kern["us_best"], 4)}
+def vs_ceiling(kern, ceil, out=None):
+    """A kernel's timing against the same-size read timed in its rotation
+    and, given `out`, against that read followed by the kernel's output
+    store (the same number of 2-byte values)."""
+    d = {"ceiling_us": ceil["us"], "ceiling_us_best": ceil["us_best"],
+         "of_ceiling": round(ceil["us"] / kern["us"], 4),
+         "of_ceiling_best": round(ceil["us_best"] / kern["us_best"], 4)}
+    if out is not None:
+        d.update({"ceiling_out_us": out["us"], "ceiling_out_us_best": out["us_best"],
+                  "of_ceiling_out": round(out["us"] / kern["us"], 4)})
+    return d
 
 
 def bench_floor(torch, kq, dev, timer, res):
@@ -444,7 +469,8 @@ def bench_roofline(torch, kq, dev, timer, ceil, res):
     g = graph_of(torch, one)
     b = int4_bytes(M, K)
     cv, hold = ceil.variant(f"int4_{b / 1e6:.2f}MB", b, N_LAYERS)
-    r = timer.round_robin({"gemv": (g.replay, 5, N_LAYERS), "ceiling": cv})
+    cvo, hold_o = ceil.variant_out(f"int4_{b / 1e6:.2f}MB", b, N_LAYERS, M)
+    r = timer.round_robin({"gemv": (g.replay, 5, N_LAYERS), "ceiling": cv, "ceiling_out": cvo})
     us = r["gemv"]["us"]
     res["roofline"] = {"bound": "hbm", "achieved": round(b / us / 1e3, 1), "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
@@ -452,8 +478,8 @@ def bench_roofline(torch, kq, dev, timer, ceil, res):
                        "bytes_per_launch": b, "us_per_launch": us,
                        "us_per_launch_best_span": r["gemv"]["us_best"],
                        "launches_timed": 5 * ROUNDS * N_LAYERS,
-                       **vs_ceiling(r["gemv"], r["ceiling"])}
-    del layers, hold
+                       **vs_ceiling(r["gemv"], r["ceiling"], r["ceiling_out"])}
+    del layers, hold, hold_o
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "int4_gemv_4096x14336_traffic.json")
@@ -715,6 +741,9 @@ def bench_vq(torch, kq, dev, args, timer, ceil, res):
         cv, hold = ceil.variant(f"vq_{b / 1e6:.2f}MB", b, N_LAYERS)
         holds.append(hold)
         variants[f"ceiling_{sh}"] = cv
+        cv, hold = ceil.variant_out(f"vq_{b / 1e6:.2f}MB", b, N_LAYERS, M)
+        holds.append(hold)
+        variants[f"ceiling_out_{sh}"] = cv
     r = timer.round_robin(variants)
     for sh, b in nbytes.items():
         k, ki = r[sh], r[f"int4_{sh}"]
@@ -724,7 +753,7 @@ def bench_vq(torch, kq, dev, args, timer, ceil, res):
                        frac=round(b / k["us"] / 1e3 / HBM_PEAK_GBS, 4), bytes=b,
                        int4_us=ki["us"], int4_bytes=bi,
                        time_per_byte_vs_int4=round((k["us"] / b) / (ki["us"] / bi), 3),
-                       **vs_ceiling(k, r[f"ceiling_{sh}"]))
+                       **vs_ceiling(k, r[f"ceiling_{sh}"], r[f"ceiling_out_{sh}"]))
     del holds, variants
     # the quantiser that makes this format (vq-gemv/quant/pq_quantize.py:28-83)
     # from dense N(0, 0.02) weights: 14336 x 4096, reference defaults (25

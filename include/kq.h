@@ -130,6 +130,15 @@ kq_status kq_stream_read(const void* src, size_t bytes, uint32_t* sink, kq_strea
 kq_status kq_stream_read_cfg(const void* src, size_t bytes, uint32_t* sink, uint32_t unroll,
                              uint32_t threads, kq_stream_t stream);
 
+/* kq_stream_read_cfg that then writes `out_elems` 2-byte values to out: lane
+ * 0 of every wave of the grid writes its fold to out[w], out[w + waves], ...
+ * -- a GEMV's output store (y of out_elems rows, written from every XCD)
+ * after the same read. No counterpart in the reference: a measurement entry,
+ * so that a kernel that must store its output is also compared with a read
+ * that pays for the same store at the end of its launch. */
+kq_status kq_stream_read_out(const void* src, size_t bytes, uint16_t* out, uint32_t out_elems,
+                             uint32_t unroll, uint32_t threads, kq_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Codebook (VQ, d = 2, 256 entries) dequant-GEMV
  *

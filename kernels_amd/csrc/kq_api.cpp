@@ -221,6 +221,17 @@ kq_status kq_stream_read_cfg(const void* src, size_t bytes, uint32_t* sink, uint
                                              reinterpret_cast<hipStream_t>(stream)));
 }
 
+kq_status kq_stream_read_out(const void* src, size_t bytes, uint16_t* out, uint32_t out_elems,
+                             uint32_t unroll, uint32_t threads, kq_stream_t stream) {
+    if (!src || !out) return KQ_ENULL;
+    if (bytes == 0 || bytes % 16 || out_elems == 0) return KQ_EINVAL;
+    if (!(unroll == 1 || unroll == 2 || unroll == 4 || unroll == 8)) return KQ_EINVAL;
+    if (threads == 0 || threads % 256 || threads > (1u << 30)) return KQ_EINVAL;
+    if (!aligned(src, 16) || !aligned(out, 2)) return KQ_EALIGN;
+    return hip_status(kq::launch_stream_read(src, bytes, nullptr, unroll, threads,
+                                             reinterpret_cast<hipStream_t>(stream), out, out_elems));
+}
+
 kq_status kq_vq_gemv(const uint8_t* IDX, const uint16_t* C, const uint16_t* S, const uint16_t* X,
                      void* Y, kq_dtype y_dtype, uint32_t M, uint32_t K, uint32_t rows_per_cb,
                      uint32_t scale_group, uint32_t batch, kq_stream_t stream) {

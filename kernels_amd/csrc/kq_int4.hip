@@ -403,9 +403,16 @@ bool make_vplan(uint32_t M, uint32_t K, uint32_t ntok, Int4Cfg cfg, VPlan& out) 
                     vlds_x(ntok, nchp) + (P > 1 ? (size_t)rounds * waves * R * ntok * 4 : 0);
                 if (lds > kLdsMax) continue;
                 // per-CU KiB plus a latency term for short waves: fewer than 8
-                // waves or fewer than 2 items leave HBM idle.
+                // waves leave HBM idle while their rings refill. At 1-2 tokens
+                // not when every item of a wave is in its ring from the start:
+                // more waves then only add a K-part reduction (1024 x 4096:
+                // 4 waves of 2 items 2.83 us, 8 waves of 1 item in 2 parts
+                // 3.00), as long as 4 waves keep every SIMD busy. At 3-4
+                // tokens the compute per item triples and the term stays
+                // (4097 x 1024 at 3 tokens: 5.11 us with it, 5.53 without).
                 double cost = (double)nreal * waves * R;
-                if (waves < 8) cost *= 1.0 + 0.1 * (8 - waves);
+                if (waves < 8 && (ntok >= 3 || nreal > D)) cost *= 1.0 + 0.1 * (8 - waves);
+                if (waves < 4 && ntok <= 2) cost *= 1.0 + 0.1 * (4 - waves);
                 // up to 16 waves: one row a wave (twice the waves of two) measured 1-3%
                 // faster when a CU's rows fit in one round (4096 x 14336, 4096 x 4096)
                 if (waves < 16) cost *= 1.0 + 0.005 * (16 - waves);
@@ -650,10 +657,16 @@ hipError_t launch_xsum32(const uint16_t* X, float* xs, uint32_t K, uint32_t batc
 // count and keeps the best (int4-gemv/src/main.mm:294-334); so does
 // bench.py. Default shape: U = 1 over 2048 x 256 threads, the best of that
 // sweep on MI355X (1 GiB: 7.0 TB/s against 5.9 for U = 4 over 8192 x 256).
+// With OUT, lane 0 of every wave then writes the wave's fold as a 2-byte
+// value to out[w], out[w + waves], ... below nout: the read with a GEMV's
+// output store, spread over the grid as a GEMV's rows are. Any launch that
+// stores from every XCD pays for that at its end (the write-back of each
+// XCD's dirty L2 lines), which the pure read does not.
 // ---------------------------------------------------------------------------
-template <int U>
+template <int U, bool OUT>
 __global__ __launch_bounds__(256) void stream_read_k(const u32x4* __restrict__ src, size_t nq,
-                                                     uint32_t* __restrict__ sink) {
+                                                     uint32_t* __restrict__ sink,
+                                                     uint16_t* __restrict__ out, uint32_t nout) {
     u32x4 a[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) a[u] = u32x4{0, 0, 0, 0};
@@ -672,23 +685,38 @@ __global__ __launch_bounds__(256) void stream_read_k(const u32x4* __restrict__ s
 #pragma unroll
     for (int u = 1; u < U; ++u) acc ^= a[u];
     const uint32_t r = acc.x ^ acc.y ^ acc.z ^ acc.w;
-    if (r == 0xFFFFFFFFu) sink[0] = r;
+    if constexpr (OUT) {
+        if ((threadIdx.x & 63) == 0) {
+            const uint32_t waves = gridDim.x * 4;
+            for (uint32_t o = (blockIdx.x * 256 + threadIdx.x) >> 6; o < nout; o += waves)
+                out[o] = (uint16_t)(r + (r >> 16));
+        }
+    } else {
+        if (r == 0xFFFFFFFFu) sink[0] = r;
+    }
+}
+
+template <bool OUT>
+hipError_t stream_read_go(const u32x4* p, size_t nq, uint32_t* sink, uint16_t* out, uint32_t nout,
+                          uint32_t unroll, unsigned blocks, hipStream_t s) {
+    switch (unroll) {
+        case 1: stream_read_k<1, OUT><<<blocks, 256, 0, s>>>(p, nq, sink, out, nout); break;
+        case 2: stream_read_k<2, OUT><<<blocks, 256, 0, s>>>(p, nq, sink, out, nout); break;
+        case 4: stream_read_k<4, OUT><<<blocks, 256, 0, s>>>(p, nq, sink, out, nout); break;
+        case 8: stream_read_k<8, OUT><<<blocks, 256, 0, s>>>(p, nq, sink, out, nout); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, uint32_t unroll,
-                              uint32_t threads, hipStream_t s) {
+                              uint32_t threads, hipStream_t s, uint16_t* out, uint32_t nout) {
     const size_t nq = bytes / 16;
     if (unroll == 0) unroll = 1;
     const unsigned blocks = threads ? threads / 256 : 2048;
     const u32x4* p = reinterpret_cast<const u32x4*>(src);
-    switch (unroll) {
-        case 1: stream_read_k<1><<<blocks, 256, 0, s>>>(p, nq, sink); break;
-        case 2: stream_read_k<2><<<blocks, 256, 0, s>>>(p, nq, sink); break;
-        case 4: stream_read_k<4><<<blocks, 256, 0, s>>>(p, nq, sink); break;
-        case 8: stream_read_k<8><<<blocks, 256, 0, s>>>(p, nq, sink); break;
-        default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    if (out) return stream_read_go<true>(p, nq, sink, out, nout, unroll, blocks, s);
+    return stream_read_go<false>(p, nq, sink, nullptr, 0, unroll, blocks, s);
 }
 
 }  // namespace kq

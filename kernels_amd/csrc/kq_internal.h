@@ -53,7 +53,8 @@ hipError_t launch_int4_scalar(const uint32_t* W, const uint16_t* S, const uint16
 hipError_t launch_xsum32(const uint16_t* X, float* xs, uint32_t K, uint32_t batch, hipStream_t s);
 // unroll 0 and threads 0: the default shape (U = 1, 2048 x 256 threads)
 hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, uint32_t unroll,
-                              uint32_t threads, hipStream_t s);
+                              uint32_t threads, hipStream_t s, uint16_t* out = nullptr,
+                              uint32_t nout = 0);
 
 bool vq_supported(uint32_t M, uint32_t K, uint32_t rows_per_cb);
 hipError_t launch_vq(const uint8_t* IDX, const uint16_t* C, const uint16_t* S, const uint16_t* X,

@@ -24,7 +24,7 @@ MOE_WS_ERR_OFFSET = 128  # KQ_MOE_WS_ERR_OFFSET
 # every symbol include/kq.h declares
 EXPORTS = ("kq_status_str", "kq_last_hip_error", "kq_version", "kq_int4_gemv",
            "kq_int4_gemv_path", "kq_int4_gemv_cfg", "kq_xsum32", "kq_stream_read",
-           "kq_stream_read_cfg",
+           "kq_stream_read_cfg", "kq_stream_read_out",
            "kq_vq_gemv", "kq_moe_default_desc", "kq_moe_workspace_size",
            "kq_moe_workspace_init", "kq_moe_workspace_error", "kq_moe_router_topk", "kq_moe_gate_up_swiglu",
            "kq_moe_down_combine", "kq_moe_block", "kq_moe_block_path", "kq_moe_block_noalloc",
@@ -75,6 +75,7 @@ def lib():
         L.kq_xsum32.argtypes = [vp, vp, u32, u32, vp]
         L.kq_stream_read.argtypes = [vp, sz, vp, vp]
         L.kq_stream_read_cfg.argtypes = [vp, sz, vp, u32, u32, vp]
+        L.kq_stream_read_out.argtypes = [vp, sz, vp, u32, u32, u32, vp]
         L.kq_vq_gemv.argtypes = [vp, vp, vp, vp, vp, i32, u32, u32, u32, u32, u32, vp]
         L.kq_moe_default_desc.argtypes = [C.POINTER(MoEDesc)]
         L.kq_moe_default_desc.restype = None
@@ -198,6 +199,13 @@ def stream_read(src, nbytes, sink, stream=None, unroll=0, threads=0):
     else:
         _check(lib().kq_stream_read(_ptr(src), nbytes, _ptr(sink), _stream(stream)),
                "kq_stream_read")
+
+
+def stream_read_out(src, nbytes, out, out_elems, unroll, threads, stream=None):
+    """The streaming read, then out_elems 2-byte values written across the
+    grid (a GEMV's output store): the ceiling of a kernel that stores y."""
+    _check(lib().kq_stream_read_out(_ptr(src), nbytes, _ptr(out), out_elems, unroll, threads,
+                                    _stream(stream)), "kq_stream_read_out")
 
 
 # ---------------------------------------------------------------------------

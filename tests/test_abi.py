@@ -243,3 +243,10 @@ def test_stream_read_and_xsum_reject_on_host():
     assert L.kq_stream_read_cfg(FAKE, 1024, FAKE, 4, 0, None) == kq.KQ_EINVAL
     assert L.kq_stream_read_cfg(FAKE + 4, 1024, FAKE, 4, 256, None) == kq.KQ_EALIGN
     assert L.kq_stream_read_cfg(None, 1024, FAKE, 4, 256, None) == kq.KQ_ENULL
+    assert L.kq_stream_read_out(None, 1024, FAKE, 16, 1, 256, None) == kq.KQ_ENULL
+    assert L.kq_stream_read_out(FAKE, 1024, None, 16, 1, 256, None) == kq.KQ_ENULL
+    assert L.kq_stream_read_out(FAKE, 1000, FAKE, 16, 1, 256, None) == kq.KQ_EINVAL  # bytes % 16
+    assert L.kq_stream_read_out(FAKE, 1024, FAKE, 0, 1, 256, None) == kq.KQ_EINVAL  # no outputs
+    assert L.kq_stream_read_out(FAKE, 1024, FAKE, 16, 3, 256, None) == kq.KQ_EINVAL  # unroll
+    assert L.kq_stream_read_out(FAKE, 1024, FAKE, 16, 1, 300, None) == kq.KQ_EINVAL  # threads
+    assert L.kq_stream_read_out(FAKE, 1024, FAKE + 1, 16, 1, 256, None) == kq.KQ_EALIGN

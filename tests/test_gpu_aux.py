@@ -83,6 +83,31 @@ def test_stream_read_reads_every_quad(gpu, nbytes, unroll, threads):
     assert sink.item() == SENTINEL, "read past the range"
 
 
+@pytest.mark.parametrize("nbytes,out_elems,threads", [(1 << 20, 4096, 2048 * 256),
+                                                       (1 << 20, 20000, 2048 * 256),
+                                                       (4096, 7, 256)])
+def test_stream_read_out_writes_exactly_its_outputs(gpu, nbytes, out_elems, threads):
+    """kq_stream_read_out writes out[0:out_elems] (each wave's fold: 0 over a
+    zero buffer; 20000 outputs over 8192 waves: some waves write three) and
+    nothing past it; an all-ones word in quad 0, read by lane 0 of wave 0,
+    reaches wave 0's outputs (out[0], out[waves], ...) as 0xFFFF + 0xFFFF =
+    0xFFFE (low 16 bits)."""
+    buf = torch.zeros(nbytes // 4, dtype=torch.int32, device=gpu)
+    out = torch.full((out_elems + 64,), 0x2468, dtype=torch.int16, device=gpu)
+    kq.stream_read_out(buf, nbytes, out, out_elems, 1, threads)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy().view(np.uint16)
+    assert (o[:out_elems] == 0).all()
+    assert (o[out_elems:] == 0x2468).all()
+    buf[0] = -1
+    kq.stream_read_out(buf, nbytes, out, out_elems, 1, threads)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy().view(np.uint16)
+    want = np.zeros(out_elems, dtype=np.uint16)
+    want[::threads // 64] = 0xFFFE
+    assert (o[:out_elems] == want).all() and (o[out_elems:] == 0x2468).all()
+
+
 def test_stream_read_fold_cancels(gpu):
     """Two all-ones words in the same thread's loads cancel in the XOR fold:
     the sink stays untouched (the fold is really over the loaded values)."""
