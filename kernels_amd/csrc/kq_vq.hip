@@ -64,6 +64,9 @@ struct QPlan {
 // lookup's address one byte permute of the index word (vq_word_perm: 2 VALU a
 // lookup instead of 3; 32 copies at a 128-byte stride took a shift and an add).
 constexpr uint32_t kCbCopies = 64;
+// Waves that load the codebook blocks and store their copies (16 copy groups
+// of 4 copies per block, so each stores 16 / kCbStagers groups).
+constexpr uint32_t kCbStagers = 4;
 
 template <int R>
 struct QSlot {
@@ -143,14 +146,24 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
     const rsrc_t rS = make_rsrc(A.S + (size_t)row0 * A.spr, rows_wg * srowb);
     const rsrc_t rX = make_rsrc(A.X, NB * A.K * 2);
 
-    // ---- 1. x and codebook loads first (vmcnt retires in order), then the ring
-    const uint32_t xtotal = NB * nw;
+    // ---- 1. x and codebook loads first (vmcnt retires in order), then the
+    // ring. Only the first waves stage: x by about ceil(words / 256) waves
+    // (4 16-byte words a thread), the codebook blocks by the first
+    // kCbStagers (the other waves' codebook loads fall out of range: no
+    // bytes); the non-stagers issue their ring loads right after, instead of
+    // behind an x load and a whole codebook block each.
+    const uint32_t xtotal = NB * nw, nwv = nthr >> 6;
+    const uint32_t xw = min(nwv, (xtotal + 255) / 256), xthr = xw * 64;
+    const uint32_t cw = min(nwv, kCbStagers);
+    const bool xst = wave < xw, cst = wave < cw;  // uniform
     u32x4 sv[kQXr];
+    if (xst) {
 #pragma unroll
-    for (int r = 0; r < kQXr; ++r) {
-        if ((uint32_t)r * nthr < xtotal) {  // uniform
-            const uint32_t w = r * nthr + tid;
-            sv[r] = __builtin_amdgcn_raw_buffer_load_b128(rX, w < xtotal ? w * 16 : kOOB, 0, 0);
+        for (int r = 0; r < kQXr; ++r) {
+            if ((uint32_t)r * xthr < xtotal) {  // uniform
+                const uint32_t w = r * xthr + tid;
+                sv[r] = __builtin_amdgcn_raw_buffer_load_b128(rX, w < xtotal ? w * 16 : kOOB, 0, 0);
+            }
         }
     }
     // codebook blocks of this workgroup's rows (only those: the LDS area has
@@ -180,10 +193,14 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
             cbv[r] = Cw[i < cb_items ? i : cbn - 1];
         }
     } else {
+        // every wave issues the loads (a conditional load left the compiler
+        // copying its registers, and so waiting for it, before the ring
+        // loads); only the stagers' are in range
         const rsrc_t rC = make_rsrc(Cw, ncb * 1024);
 #pragma unroll
         for (int b = 0; b < 2; ++b)
-            cbq[b] = __builtin_amdgcn_raw_buffer_load_b128(rC, lane * 16 + (b < (int)ncb ? b * 1024u : kOOB), 0, 0);
+            cbq[b] = __builtin_amdgcn_raw_buffer_load_b128(
+                rC, lane * 16 + (cst && b < (int)ncb ? b * 1024u : kOOB), 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -227,23 +244,25 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
 
     // ---- 2. finish staging: x (as loaded: index i meets dword i), zero
     // padding, codebooks
+    if (xst) {
 #pragma unroll
-    for (int r = 0; r < kQXr; ++r) {
-        if ((uint32_t)r * nthr < xtotal) {  // uniform
-            const uint32_t w = r * nthr + tid;
+        for (int r = 0; r < kQXr; ++r) {
+            if ((uint32_t)r * xthr < xtotal) {  // uniform
+                const uint32_t w = r * xthr + tid;
+                if (w < xtotal) {
+                    const uint32_t t = w / nw, wi = w - t * nw, ch = wi >> 2;
+                    *reinterpret_cast<u32x4*>(xs + ((ch >> 6) * NB + t) * kQBlk + (wi & 3) * 1024 +
+                                              (ch & 63) * 16) = sv[r];
+                }
+            }
+        }
+        for (uint32_t w0 = kQXr * xthr; w0 < xtotal; w0 += xthr) {  // past 8 words a thread
+            const uint32_t w = w0 + tid;
             if (w < xtotal) {
                 const uint32_t t = w / nw, wi = w - t * nw, ch = wi >> 2;
                 *reinterpret_cast<u32x4*>(xs + ((ch >> 6) * NB + t) * kQBlk + (wi & 3) * 1024 +
-                                          (ch & 63) * 16) = sv[r];
+                                          (ch & 63) * 16) = reinterpret_cast<const u32x4*>(A.X)[w];
             }
-        }
-    }
-    for (uint32_t w0 = kQXr * nthr; w0 < xtotal; w0 += nthr) {  // only past 8 words per thread
-        const uint32_t w = w0 + tid;
-        if (w < xtotal) {
-            const uint32_t t = w / nw, wi = w - t * nw, ch = wi >> 2;
-            *reinterpret_cast<u32x4*>(xs + ((ch >> 6) * NB + t) * kQBlk + (wi & 3) * 1024 +
-                                      (ch & 63) * 16) = reinterpret_cast<const u32x4*>(A.X)[w];
         }
     }
     const uint32_t npad = nchp - nch;
@@ -261,19 +280,18 @@ __global__ __launch_bounds__(1024) void vq_valu(QArgs A) {
         }
         for (uint32_t i = kCbPre * nthr + tid; i < cb_items; i += nthr) cb[i] = Cw[i];
     } else {
-        // copy group g = copies 4g .. 4g + 3 of an entry (16 groups). Wave w
-        // stores groups (w' + l) % 16 of the lane's 4 entries for w' = w, w +
-        // waves, ... < 16: an entry's 64 copies span the 64 banks, so the 16
-        // lanes of a quarter-wave write 16 different groups (no conflicts),
-        // and over w' every (entry, group) is written once.
+        // copy group g = copies 4g .. 4g + 3 of an entry (16 groups). Stager
+        // wave w stores groups (w' + l) % 16 of the lane's 4 entries for w' =
+        // w, w + cw, ... < 16: an entry's 64 copies span the 64 banks, so the
+        // 16 lanes of a quarter-wave write 16 different groups (no
+        // conflicts), and over w' every (entry, group) is written once.
         static_assert(CR == 64, "copy-group stores assume 64 copies");
-        const uint32_t nwv = nthr >> 6;
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            if (b >= (int)ncb) break;  // uniform
+            if (!cst || b >= (int)ncb) break;  // uniform
             const uint32_t ev[4] = {cbq[b].x, cbq[b].y, cbq[b].z, cbq[b].w};
             uint32_t* eb = cb + ((uint32_t)b * 256 + lane * 4) * CR;  // the lane's first entry
-            for (uint32_t w2 = wave; w2 < 16; w2 += nwv) {  // uniform
+            for (uint32_t w2 = wave; w2 < 16; w2 += cw) {  // uniform
                 const uint32_t g = (w2 + lane) & 15;
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
