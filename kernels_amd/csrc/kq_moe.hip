@@ -1482,6 +1482,7 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
     __shared__ uint32_t s_idx[kMaxSlots];
     __shared__ float s_wgt[kMaxSlots];
     __shared__ uint32_t bits[8];
+    __shared__ uint32_t s_next;  // next item of the workgroup's range to hand out
     const uint32_t K = d.hidden, IN = d.inter, TK = d.top_k;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1511,51 +1512,45 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
         if (pa.u != 0xFFFFFFFFu) pr = PartRange{pa.u * IN + pa.r0, pa.nr};
     }
     const uint32_t N = pr.n;
-    const uint32_t nit = N > wave ? (N - wave + kStWaves - 1) / kStWaves : 0;
     const uint32_t nexp = min(ps.n, batch * TK);
     if (nexp == 0) return;  // uniform (never: every token selects top_k experts)
-    // item cursors (u, i), advanced by kStWaves items without division
     struct Cur {
         uint32_t u, i;
     };
-    auto adv = [&](Cur& c) __attribute__((always_inline)) {
-        c.i += kStWaves;
-        while (c.i >= IN) {  // uniform
-            c.i -= IN;
-            ++c.u;
-        }
+    // Item k of the workgroup's range -> (plan entry u, row i): a multiply by
+    // 2^32 / IN rounded up, exact here (pr.g0 + k < 2^32 / IN) and checked once.
+    const uint32_t inv_in = 0xFFFFFFFFu / IN + 1u;
+    auto item = [&](uint32_t k) __attribute__((always_inline)) {
+        const uint32_t g = pr.g0 + k;
+        uint32_t u = __umulhi(g, inv_in);
+        if ((u + 1) * IN <= g) ++u;
+        return Cur{u, g - u * IN};
     };
-    const uint32_t gw = pr.g0 + wave;
-    Cur ci{gw / IN, gw % IN}, cc = ci, clast = ci;
 
-    // 4. prime the ring
+    // 4. prime the ring: a wave's first D items are items wave, wave + 8, ...;
+    // every later one goes out through an LDS counter to whichever wave
+    // refills a slot first (the SIMDs issue for their older waves first, and
+    // a fixed deal left the younger waves behind at the end). An item past
+    // the range loads through an empty descriptor (no traffic, the same load
+    // count).
     const StLane<J> L = st_lane<J>(half ? d.off_up : d.off_gate, d, K, 0, 0, 0);
     constexpr int D = kPartD;
-    StSlot<J> ring[D];
-    uint32_t nis = 0;
-    auto issue = [&](StSlot<J>& e) __attribute__((always_inline)) {
-        // padding re-reads the last item; a wave without items loads its first
-        // position's row (clamped to a valid entry)
-        if (nis < nit) clast = ci;
+    static_assert(D == 3, "the loop body is written for three slots");
+    auto issue_k = [&](StSlot<J>& e, uint32_t k) __attribute__((always_inline)) {
+        const bool ok = k < N;  // uniform
+        const Cur c = item(ok ? k : 0);
         const uint32_t ex = __builtin_amdgcn_readfirstlane(
-            min(ps.expert[min(clast.u, nexp - 1)], d.n_experts - 1));
-        const rsrc_t r = make_rsrc(pool + (size_t)ex * d.blob, (uint32_t)d.blob);
-        const uint32_t i = __builtin_amdgcn_readfirstlane(min(clast.i, IN - 1));
+            min(ps.expert[min(c.u, nexp - 1)], d.n_experts - 1));
+        const rsrc_t r = make_rsrc(pool + (size_t)ex * d.blob, ok ? (uint32_t)d.blob : 0u);
+        const uint32_t i = __builtin_amdgcn_readfirstlane(min(c.i, IN - 1));
         st_issue<J>(e, r, L, i * rowb, i * metab, i * 2);
-        adv(ci);
-        ++nis;
     };
-#pragma unroll
-    for (int q = 0; q < D; ++q) {
-        issue(ring[q]);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    // 5. staging store (vector = token), chunks past K zero
-    st_stage_store<J>(st, act, batch, K);
-    __syncthreads();
-    if (nit == 0) return;  // no later barrier
 
-    // 6. stream
+    // 5, 6. prime the ring, store the staged x (vector = token, chunks past
+    // K zero), then stream. Each form below primes its own ring (one primed
+    // before the choice left the other copying its registers, and so waiting
+    // for every load, at its loop head); the choice is uniform in the
+    // workgroup, so the barrier inside it is too.
     const DequantConsts kc;
     // One store per step by every lane (lane j < the item's slot count: slot
     // j; the rest repeat the last), so the next ring wait does not also wait
@@ -1563,22 +1558,57 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
     // entry chosen by one slot, the common case): the token's x chunks are
     // held in registers, so the loop reads no LDS.
     const uint32_t ua = pr.g0 / IN, ub = (pr.g0 + N - 1) / IN;
+    // The draw: an LDS atomic by lane 0 alone, exec narrowed and restored
+    // inside one asm block that also waits for the return (a one-lane atomic
+    // written as a branch left the waitcnt pass waiting for every load at
+    // the loop head; a return left in flight in a register past the asm could
+    // be copied before it arrives); lane 0's value is made uniform outside it.
+    const uint32_t next_a =
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&s_next;
+    auto draw = [&]() __attribute__((always_inline)) {
+        uint32_t v;
+        uint64_t saved;
+        asm volatile(
+            "s_mov_b64 %1, exec\n\t"
+            "s_mov_b64 exec, 1\n\t"
+            "ds_add_rtn_u32 %0, %2, %3\n\t"
+            "s_mov_b64 exec, %1\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(v), "=&s"(saved)
+            : "v"(next_a), "v"(1u)
+            : "memory");
+        return __builtin_amdgcn_readfirstlane(v);
+    };
     auto run = [&](auto xr_tag) __attribute__((always_inline)) {
         constexpr bool XR = decltype(xr_tag)::value;
+        StSlot<J> ring[D];
+        uint32_t sk[D];  // the item each ring slot holds
+#pragma unroll
+        for (int q = 0; q < D; ++q) {
+            sk[q] = wave + q * kStWaves;
+            issue_k(ring[q], sk[q]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (threadIdx.x == 0) s_next = D * kStWaves;
+        st_stage_store<J>(st, act, batch, K);
+        __syncthreads();
+        if (wave >= N) return;  // no items; no later barrier
         StX<J> xr;
         if constexpr (XR) {
             uint64_t ma = ps.mask[ua][0], mb = ps.mask[ua][1];
             st_xload<J>(xr, act, pop_slot(ma, mb) / TK);
         }
-        auto step = [&](const StSlot<J>& e, uint32_t it, bool tail) __attribute__((always_inline)) {
-            if (tail && it >= nit) return;  // padding (uniform)
-            const Cur c = cc;
-            adv(cc);
+        // a step draws the item its slot takes next between its plan read
+        // and its first use of the weights (far longer than an LDS atomic)
+        auto step = [&](const StSlot<J>& e, const Cur c, uint32_t& nk) __attribute__((always_inline)) {
+            uint64_t ma = ps.mask[c.u][0], mb = ps.mask[c.u][1];
+            __builtin_amdgcn_sched_barrier(0);
+            nk = draw();
+            __builtin_amdgcn_sched_barrier(0);
             StDq<J> q;
             if constexpr (!XR) st_dequant<J>(e, kc, q);
             const float bg = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 0));
             const float bu = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 32));
-            uint64_t ma = ps.mask[c.u][0], mb = ps.mask[c.u][1];
             const uint32_t nv = XR ? 1u : (uint32_t)(__popcll(ma) + __popcll(mb));
             size_t oi = 0;
             uint16_t ov = 0;
@@ -1596,17 +1626,32 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
             }
             H[oi] = ov;
         };
-        const uint32_t nsteps = (nit + D - 1) / D * D;
-        uint32_t it = 0;
-        for (; it + D < nsteps; it += D) {
-#pragma unroll
-            for (int q = 0; q < D; ++q) {
-                step(ring[q], it + q, false);
-                issue(ring[q]);
-            }
+        // every step refills its slot (an item past the range moves no
+        // bytes), so the loop body has one path; a wave's items only grow,
+        // so the first slot past the range ends its stream
+        // a slot past the range stores once through an empty descriptor
+        // (dropped) and refills out of range, so every path through the loop
+        // issues the same stores and loads and each wait counts exactly the
+        // other slots'
+        const rsrc_t rnull = make_rsrc(H, 0);
+        auto slot = [&](int s, bool live) __attribute__((always_inline)) {
+            uint32_t nk = N;
+            if (live) step(ring[s], item(sk[s]), nk);  // uniform
+            else __builtin_amdgcn_raw_buffer_store_b16((uint16_t)0, rnull, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            sk[s] = nk;
+            issue_k(ring[s], nk);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        // One exit, at the top: with an exit after each slot the compiler
+        // sank a slot's refill loads past the next exit test (they are dead
+        // on that path) and past the next slot's work. A slot past the range
+        // means every later slot is, and so is the refilled slot 0.
+        while (sk[0] < N) {  // uniform
+            slot(0, true);
+            slot(1, sk[1] < N);
+            slot(2, sk[2] < N);
         }
-#pragma unroll
-        for (int q = 0; q < D; ++q) step(ring[q], it + q, true);
     };
     // (at J = 4 the registers of the one-slot form would spill)
     const bool one = ua == ub && __popcll(ps.mask[ua][0]) + __popcll(ps.mask[ua][1]) == 1;
@@ -1630,6 +1675,7 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_part_k(
     const Plan* __restrict__ plan_g, const uint16_t* __restrict__ H, uint32_t nslots,
     float* __restrict__ ys) {
     extern __shared__ __align__(16) unsigned char act[];  // [nvec h blocks]
+    __shared__ uint32_t s_next;  // next row pair of the workgroup's range to hand out
     const uint32_t HID = d.hidden, K = d.inter, nw = K >> 3, nch = K >> 5;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1640,7 +1686,6 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_part_k(
     const uint64_t mk0 = pa.m0, mk1 = pa.m1;
     const uint32_t nvec = __popcll(mk0) + __popcll(mk1);
     const uint32_t p0 = pa.r0, np = pa.nr;
-    const uint32_t nit = np > wave ? (np - wave + kStWaves - 1) / kStWaves : 0;
 
     // 1. the expert's h vectors, slot order: word tid of vector k (K <= 4096: nw <= threads)
     const rsrc_t rh = make_rsrc(H, nslots * K * 2);
@@ -1656,25 +1701,32 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_part_k(
             }
         }
     }
-    // 2. prime the ring: row pairs p0 + wave, + kStWaves, ... of one expert
+    // 2. prime the ring: a wave's first D items are row pairs p0 + wave,
+    // + kStWaves, ... of the expert; every later one goes out through an LDS
+    // counter to whichever wave refills a slot first (the SIMDs issue for
+    // their older waves first, and a fixed deal left the younger waves
+    // behind at the end). An item past the range loads through an empty
+    // descriptor (no traffic, the same load count).
     const StLane<J> L = st_lane<J>(d.off_down, d, K, half * rowb, half * metab, half * 2);
     const rsrc_t r = make_rsrc(pool + (size_t)ex * d.blob, (uint32_t)d.blob);
+    const rsrc_t rw0 = make_rsrc(pool + (size_t)ex * d.blob, 0u);
     constexpr int D = kPartD;
+    static_assert(D == 3, "the loop body is written for three slots");
     StSlot<J> ring[D];
-    uint32_t nis = 0;
-    auto issue = [&](StSlot<J>& e) __attribute__((always_inline)) {
-        // padding re-reads the last item; a wave without items loads pair p0
-        const uint32_t it = nit ? min(nis, nit - 1) : 0u;
-        const uint32_t pr = nit ? p0 + wave + it * kStWaves : p0;
-        st_issue<J>(e, r, L, 2 * pr * rowb, 2 * pr * metab, 2 * pr * 2);
-        ++nis;
+    uint32_t sk[D];  // the item (row pair - p0) each ring slot holds
+    auto issue_k = [&](StSlot<J>& e, uint32_t k) __attribute__((always_inline)) {
+        const bool ok = k < np;  // uniform
+        const uint32_t pr = p0 + (ok ? k : 0u);
+        st_issue<J>(e, ok ? r : rw0, L, 2 * pr * rowb, 2 * pr * metab, 2 * pr * 2);
     };
     // primed on every path (same load count: the staging waits only for its own loads)
 #pragma unroll
     for (int q = 0; q < D; ++q) {
-        issue(ring[q]);
+        sk[q] = wave + q * kStWaves;
+        issue_k(ring[q], sk[q]);
         __builtin_amdgcn_sched_barrier(0);
     }
+    if (tid == 0) s_next = D * kStWaves;
     // 3. staging store: permuted pairs and chunk constants, chunks past K zero
 #pragma unroll
     for (int k = 0; k < kStXr; ++k) {
@@ -1702,14 +1754,39 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_part_k(
     }
     __syncthreads();
 
+    if (wave >= np) return;  // no items; no later barrier
+
     // 4. stream
     const DequantConsts kc;
+    // The draw: an LDS atomic by lane 0 alone, exec narrowed and restored
+    // inside one asm block that also waits for the return (a one-lane atomic
+    // written as a branch left the waitcnt pass waiting for every load at
+    // the loop head; a return left in flight in a register past the asm could
+    // be copied before it arrives); lane 0's value is made uniform outside it.
+    const uint32_t next_a =
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&s_next;
+    auto draw = [&]() __attribute__((always_inline)) {
+        uint32_t v;
+        uint64_t saved;
+        asm volatile(
+            "s_mov_b64 %1, exec\n\t"
+            "s_mov_b64 exec, 1\n\t"
+            "ds_add_rtn_u32 %0, %2, %3\n\t"
+            "s_mov_b64 exec, %1\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(v), "=&s"(saved)
+            : "v"(next_a), "v"(1u)
+            : "memory");
+        return __builtin_amdgcn_readfirstlane(v);
+    };
     // One store per step by every lane: lane (h, j), j < nvec, writes slot j's
     // row 2 pr + h; the other lanes repeat the last slot's. The next ring wait
-    // then does not also wait for it; only the tail checks for padding.
-    auto step = [&](const StSlot<J>& e, uint32_t it, bool tail) __attribute__((always_inline)) {
-        if (tail && it >= nit) return;  // padding (uniform)
-        const uint32_t pr = p0 + wave + it * kStWaves;
+    // then does not also wait for it. A step draws the item its slot takes
+    // next before its first use of the weights (far longer than an LDS atomic).
+    auto step = [&](const StSlot<J>& e, uint32_t pr, uint32_t& nk) __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_barrier(0);
+        nk = draw();
+        __builtin_amdgcn_sched_barrier(0);
         StDq<J> q;
         st_dequant<J>(e, kc, q);
         const float b0 = bf2f((uint16_t)__builtin_amdgcn_readlane(e.bi, 0));
@@ -1728,18 +1805,27 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_part_k(
         }
         ys[oi] = ov;
     };
-    if (nit > 0) {
-        const uint32_t nsteps = (nit + D - 1) / D * D;
-        uint32_t it = 0;
-        for (; it + D < nsteps; it += D) {
-#pragma unroll
-            for (int q = 0; q < D; ++q) {
-                step(ring[q], it + q, false);
-                issue(ring[q]);
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < D; ++q) step(ring[q], it + q, true);
+    // a slot past the range stores once through an empty descriptor
+    // (dropped) and refills out of range, so every path through the loop
+    // issues the same stores and loads and each wait counts exactly the
+    // other slots'
+    const rsrc_t rnull = make_rsrc(ys, 0);
+    auto slot = [&](int s, bool live) __attribute__((always_inline)) {
+        uint32_t nk = np;
+        if (live) step(ring[s], p0 + sk[s], nk);  // uniform
+        else __builtin_amdgcn_raw_buffer_store_b32(0u, rnull, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        sk[s] = nk;
+        issue_k(ring[s], nk);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // One exit, at the top (an exit after each slot let the compiler sink a
+    // slot's refill loads past the next exit test). A slot past the range
+    // means every later slot is, and so is the refilled slot 0.
+    while (sk[0] < np) {  // uniform
+        slot(0, true);
+        slot(1, sk[1] < np);
+        slot(2, sk[2] < np);
     }
 }
 
