@@ -392,11 +392,17 @@ def _compact_desc(hidden, inter, n_experts, top_k):
 
 
 @pytest.mark.parametrize("hidden,inter,batch", [(1024, 2048, 1), (4096, 512, 2), (2048, 4096, 1),
-                                                (1536, 1024, 3), (2048, 2048, 4), (2048, 4096, 3)])
+                                                (1536, 1024, 3), (2048, 2048, 4), (2048, 4096, 3),
+                                                (1024, 2048, 8), (2048, 1024, 12), (4096, 512, 16),
+                                                (1536, 4096, 7)])
 def test_other_shapes(gpu, hidden, inter, batch):
     """Descriptors other than gpt-oss's (every chunk count of the streaming
     kernels, partial chunks, 16 experts, top-3): the block and the
-    standalone projections against the oracle, routing exact."""
+    standalone projections against the oracle, routing exact. From 6 tokens
+    both projections run partitioned by expert with their items handed out
+    in the workgroup, here at every chunk count (hidden 1024 / 1536 / 2048 /
+    4096 for gate/up, inter 512 / 1024 / 2048 / 4096 for down) and with
+    experts shared by several tokens."""
     d, off = _compact_desc(hidden, inter, 16, 3)
     host = gen.moe_pool(16, seed=hidden + inter, quantize=True, hidden=hidden, inter=inter,
                         blob=d.blob, off=off)
