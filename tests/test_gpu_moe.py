@@ -100,6 +100,70 @@ def test_router_ties_lowest_index(gpu):
     assert np.allclose(b.wgt.cpu().numpy()[0], owgt[0], atol=1e-6)
 
 
+NAN, NINF = float("nan"), float("-inf")
+# (experts, top-k, base logit of expert e, logits set apart, the expected picks):
+# ties across the four 64-expert columns (7 / 135, 64 / 200: the lower index
+# first), NaN and -inf never picked, -0 tying +0 (expert 2 before 3); only
+# two candidates in columns 2 and 3 (experts 128, 129); fewer candidates than
+# picks (the passes past them give expert 0 and weight 0)
+TOPK_EDGE = {
+    "wide": (256, 8, lambda e: -1.0 - e / 512,
+             {7: 5.0, 135: 5.0, 255: 4.5, 64: 4.0, 200: 4.0, 130: 3.0, 131: 3.0, 2: -0.0, 3: 0.0,
+              0: NAN, 1: NINF},
+             [7, 135, 255, 64, 200, 130, 131, 2]),
+    "ragged": (130, 4, lambda e: -e / 256, {129: 2.0, 128: 1.5, 5: 1.5}, [129, 5, 128, 0]),
+    "unselectable": (16, 8, lambda e: NAN, {10: NINF, 11: NINF, 12: NINF, 13: 1.0, 14: 3.0, 15: 2.0},
+                     [14, 15, 13, 0, 0, 0, 0, 0]),
+}
+
+
+def edge_router(ne, base, special):
+    """fp32 router weights whose logits for x = e_0 are exactly the given values."""
+    R = np.zeros((ne, 2880), np.float32)
+    R[:, 0] = [base(e) for e in range(ne)]
+    for e, v in special.items():
+        R[e, 0] = v
+    X = np.zeros((1, 2880), np.float32)
+    X[0, 0] = 1.0
+    return R, X
+
+
+@pytest.mark.parametrize("case", list(TOPK_EDGE))
+def test_router_topk_edge_logits(gpu, case):
+    """The wave top-k's columns, ties, NaN / -inf / -0 and passes with nothing
+    left to pick, against the oracle's strict-greater scan."""
+    ne, tk, base, special, want = TOPK_EDGE[case]
+    d = kq.moe_default_desc()
+    d.n_experts, d.top_k = ne, tk
+    R, X = edge_router(ne, base, special)
+    oidx, owgt, _ = oracle.moe_router(R, oracle.F32, X, oracle.F32, 1, odesc(d))
+    assert oidx[0].tolist() == want
+    b = Block(gpu, d, 1, x_f32=True)
+    kq.moe_router_topk(torch.from_numpy(R).to(gpu), torch.from_numpy(X).to(gpu), b.idx, b.wgt, d,
+                       b.ws, b.wsb, batch=1, xh=b.xh)
+    torch.cuda.synchronize()
+    assert b.idx.cpu().tolist()[0] == want
+    assert np.allclose(b.wgt.cpu().numpy()[0], owgt[0], atol=1e-6, rtol=0)
+
+
+@pytest.mark.parametrize("path", [kq.MOE_PATH_AUTO, kq.MOE_PATH_ONE, kq.MOE_PATH_ATOMIC])
+def test_block_topk_edge_logits(gpu, pool16, path):
+    """The block's own top-k (in the gate/up launch, or in the one-launch
+    kernel) on tied, NaN and -inf logits: routing and y as the oracle's."""
+    host, pool = pool16
+    d = _pool_desc(16)
+    R, X = edge_router(16, lambda e: -e / 64, {0: NAN, 1: NINF, 4: NAN, 9: 2.0, 12: 2.0, 10: 1.0, 15: 1.0})
+    oidx, owgt, Yref = oracle.moe_block(host, odesc(d), R, oracle.F32, X, oracle.F32, 1)
+    assert oidx[0].tolist() == [9, 12, 10, 15]
+    b = Block(gpu, d, 1, x_f32=True)
+    kq.moe_block(pool, d, torch.from_numpy(R).to(gpu), torch.from_numpy(X).to(gpu), b.idx, b.wgt,
+                 b.H, b.y, b.ws, b.wsb, batch=1, xh=b.xh, path=path)
+    torch.cuda.synchronize()
+    assert b.idx.cpu().tolist()[0] == [9, 12, 10, 15]
+    assert np.allclose(b.wgt.cpu().numpy()[0], owgt[0], atol=1e-6, rtol=0)
+    assert_close(to_f64(b.y), Yref, what=f"edge-logit block path {path}")
+
+
 def unfused_ws(device, d):
     wsb = kq.moe_unfused_workspace_size(d)
     return torch.empty(wsb, dtype=torch.uint8, device=device), wsb
