@@ -163,7 +163,10 @@ __device__ __forceinline__ void unpack8(const Raw8<F32>& r, float v[8]) {
 // workgroups of the same launch (device-coherent loads); otherwise from an
 // earlier launch (plain loads).
 // topk_vals: the same from the logits already in registers (lane l holds
-// experts l + 64q in x[q]).
+// experts l + 64q in x[q]). topk_lanes: the same results in registers, slot
+// j's expert and weight in lane j (lanes from TK on: expert 0, weight 0).
+__device__ __forceinline__ void topk_lanes(const float (&x)[4], uint32_t NE, uint32_t TK,
+                                           uint32_t& pj, float& wj);
 __device__ __forceinline__ void topk_vals(const float (&x)[4], uint32_t NE, uint32_t TK,
                                           uint32_t* idx_out, float* wgt_out);
 template <bool COHERENT>
@@ -181,8 +184,8 @@ __device__ __forceinline__ void topk_wave(const float* L, uint32_t NE, uint32_t 
     }
     topk_vals(x, NE, TK, idx_out, wgt_out);
 }
-__device__ __forceinline__ void topk_vals(const float (&x)[4], uint32_t NE, uint32_t TK,
-                                          uint32_t* idx_out, float* wgt_out) {
+__device__ __forceinline__ void topk_lanes(const float (&x)[4], uint32_t NE, uint32_t TK,
+                                           uint32_t& pj, float& wj) {
     const uint32_t lane = threadIdx.x & 63;
     float v[4];
 #pragma unroll
@@ -195,7 +198,7 @@ __device__ __forceinline__ void topk_vals(const float (&x)[4], uint32_t NE, uint
     // in descending order, so the largest selected logit is chosen[0].
     const float mx = chosen[0];
     float cj = -INFINITY;
-    uint32_t pj = 0;
+    pj = 0;
 #pragma unroll
     for (int j = 0; j < kMaxTopK; ++j) {
         if ((uint32_t)j < TK && lane == (uint32_t)j) {
@@ -211,9 +214,17 @@ __device__ __forceinline__ void topk_vals(const float (&x)[4], uint32_t NE, uint
     sum = dpp_fadd<0xB1>(sum);   // quad_perm [1,0,3,2]
     sum = dpp_fadd<0x4E>(sum);   // quad_perm [2,3,0,1]
     sum = dpp_fadd<0x141>(sum);  // row_half_mirror
+    wj = lane < TK ? __fdividef(ex, sum) : 0.0f;
+}
+__device__ __forceinline__ void topk_vals(const float (&x)[4], uint32_t NE, uint32_t TK,
+                                          uint32_t* idx_out, float* wgt_out) {
+    const uint32_t lane = threadIdx.x & 63;
+    uint32_t pj;
+    float wj;
+    topk_lanes(x, NE, TK, pj, wj);
     if (lane < TK) {
         idx_out[lane] = pj;
-        wgt_out[lane] = __fdividef(ex, sum);
+        wgt_out[lane] = wj;
     }
 }
 
@@ -962,11 +973,35 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
 
     StStage st;
     st_stage_load(st, xh, batch, K);
-    if constexpr (SRC == 2)
-        plan_from_logits(lg, batch, d.n_experts, TK, ps, s_idx, s_wgt);
-    else
-        get_plan<SRC == 1>(plan_g, idx, nullptr, batch * TK, d.n_experts, ps, s_idx, s_wgt, bits);
-    const uint32_t nexp = ps.n, N = nexp * IN;
+    // One token with the top-k here (RP): plan entry u is slot u, so each wave
+    // keeps the plan in registers -- lane u holds entry u's expert and weight
+    // -- and reads it by readlane: no LDS round trip stands between the logits
+    // and the first weight load (the LDS form wrote the picks, read them back,
+    // wrote the plan and read it again).
+    constexpr bool RP = SRC == 2 && XREG;
+    uint32_t rexp = 0, nexp;
+    float rwgt = 0.0f;
+    if constexpr (RP) {
+        const uint32_t NE = d.n_experts;
+        float xl[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xl[q] = lg[min(lane + 64 * q, NE - 1)];
+        topk_lanes(xl, NE, TK, rexp, rwgt);
+        nexp = TK;
+    } else {
+        if constexpr (SRC == 2)
+            plan_from_logits(lg, batch, d.n_experts, TK, ps, s_idx, s_wgt);
+        else
+            get_plan<SRC == 1>(plan_g, idx, nullptr, batch * TK, d.n_experts, ps, s_idx, s_wgt, bits);
+        nexp = ps.n;
+    }
+    // expert of plan entry u (uniform)
+    auto plan_expert = [&](uint32_t u) __attribute__((always_inline)) {
+        const uint32_t uu = min(u, nexp - 1);
+        if constexpr (RP) return min((uint32_t)__builtin_amdgcn_readlane((int)rexp, (int)uu), d.n_experts - 1);
+        else return (uint32_t)__builtin_amdgcn_readfirstlane(min(ps.expert[uu], d.n_experts - 1));
+    };
+    const uint32_t N = nexp * IN;
     const uint32_t per = (N + gridDim.x - 1) / gridDim.x, k0 = blockIdx.x * per;
     const uint32_t cnt = k0 < N ? min(per, N - k0) : 0;
     const uint32_t nit = cnt > wave ? (cnt - wave + kStWaves - 1) / kStWaves : 0;
@@ -1019,8 +1054,7 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     auto issue_k = [&](StSlot<J>& e, uint32_t k) __attribute__((always_inline)) {
         const bool ok = k < cnt;  // uniform
         const Cur c = item(ok ? k : 0);
-        const uint32_t ex =
-            __builtin_amdgcn_readfirstlane(min(ps.expert[min(c.u, nexp - 1)], d.n_experts - 1));
+        const uint32_t ex = plan_expert(c.u);
         const rsrc_t r = make_rsrc(pool + (size_t)ex * d.blob, ok ? (uint32_t)d.blob : 0u);
         const uint32_t i = __builtin_amdgcn_readfirstlane(c.i);
         st_issue<J>(e, r, L, i * rowb, i * metab, i * 2);
@@ -1028,8 +1062,7 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     uint32_t sk[D];  // the item each ring slot holds (dynamic hand-out)
     auto issue = [&](StSlot<J>& e) __attribute__((always_inline)) {
         if (nis < nit) clast = ci;  // padding re-reads the last item
-        const uint32_t ex =
-            __builtin_amdgcn_readfirstlane(min(ps.expert[min(clast.u, nexp - 1)], d.n_experts - 1));
+        const uint32_t ex = plan_expert(clast.u);
         const rsrc_t r = make_rsrc(pool + (size_t)ex * d.blob, (uint32_t)d.blob);
         const uint32_t i = __builtin_amdgcn_readfirstlane(clast.i);
         st_issue<J>(e, r, L, i * rowb, i * metab, i * 2);
@@ -1049,7 +1082,18 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
         __builtin_amdgcn_sched_barrier(0);
     }
     if (!AT && threadIdx.x == 0) s_next = D * kStWaves;
-    if constexpr (SRC == 2) {
+    if constexpr (RP) {  // what publish_plan writes, from the registers
+        if (blockIdx.x == 0 && wave == 0) {
+            if (lane < TK) {
+                idx_out[lane] = rexp;
+                wgt_out[lane] = rwgt;
+                plan_out->expert[lane] = min(rexp, d.n_experts - 1);
+                plan_out->mask[lane][0] = 1ull << lane;
+                plan_out->mask[lane][1] = 0;
+            }
+            if (lane == 0) plan_out->n = TK;
+        }
+    } else if constexpr (SRC == 2) {
         if (blockIdx.x == 0) publish_plan(ps, s_idx, s_wgt, batch * TK, idx_out, wgt_out, plan_out);
     }
     st_stage_store<J>(st, act, batch, K);
@@ -1066,7 +1110,14 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_stream_k(
     // runs between the step's plan reads and its first use of the weights.
     auto step = [&](const StSlot<J>& e, uint32_t it, bool tail, auto&& mid) __attribute__((always_inline)) {
         if (tail && it >= nit) return;  // padding (uniform)
-        uint64_t m0 = ps.mask[cc.u][0], m1 = ps.mask[cc.u][1];
+        uint64_t m0, m1;
+        if constexpr (RP) {
+            m0 = 1ull << cc.u;
+            m1 = 0;
+        } else {
+            m0 = ps.mask[cc.u][0];
+            m1 = ps.mask[cc.u][1];
+        }
         mid();
         StDq<J> q;
         st_dequant<J>(e, kc, q);
