@@ -1385,6 +1385,17 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_dn_stream_k(
 // 52.2 / 89.4 / 163.1 us per block (depth 4 held the one-slot gate/up at
 // 256 VGPRs with 3 spilled; depth 2: 51.3 / 89.9 / 166.1).
 constexpr uint32_t kPartRow = 4, kPartSlot = 5;
+// The gate/up's split (3-7 tokens) prices rows by the form that computes them:
+// a workgroup whose one entry is chosen by one slot keeps that token's x in
+// registers, faster than the LDS form of the other workgroups. Measured per
+// item at 8 tokens (us x workgroups): one slot 0.129 in registers / 0.151
+// from LDS, two slots 0.229, three 0.308, i.e. 36 for a one-slot row and
+// 21 + 22 s otherwise. Against 4 + 5 s for every row, A/B per block: 3 / 4 /
+// 5 / 6 tokens 42.96 / 51.85 / 60.98 / 69.56 -> 42.45 / 51.49 / 60.28 /
+// 68.58 us, outputs bitwise equal. (The equal-cost ranges from 8 tokens keep
+// 4 + 5 s: a workgroup whose range spans two one-slot entries runs the LDS
+// form, and the new prices then left those ~7 us behind.)
+constexpr uint32_t kGuOne = 36, kGuRow = 21, kGuSlot = 22;
 constexpr int kPartD = 3;
 struct PartAssign {
     uint32_t u, r0, nr, ex;  // u = 0xFFFFFFFF: no work for this workgroup
@@ -1414,7 +1425,8 @@ __device__ __forceinline__ uint64_t rl64(uint64_t v, uint32_t l) {
     return (uint64_t)rl((uint32_t)v, l) | ((uint64_t)rl((uint32_t)(v >> 32), l) << 32);
 }
 __device__ __forceinline__ PartAssign part_assign(const Plan* plan_g, uint32_t nslots, uint32_t nrows,
-                                                  uint32_t n_experts) {
+                                                  uint32_t n_experts, uint32_t c_one = kPartRow + kPartSlot,
+                                                  uint32_t c_row = kPartRow, uint32_t c_slot = kPartSlot) {
     const uint32_t lane = threadIdx.x & 63, G = gridDim.x, b = blockIdx.x;
     const uint64_t sb0 = slot_bits(nslots, 0), sb1 = slot_bits(nslots, 1);
     // every entry's loads first (entries past n are read but unused)
@@ -1432,9 +1444,10 @@ __device__ __forceinline__ PartAssign part_assign(const Plan* plan_g, uint32_t n
     if (n == 0 || G < n) return a;
     uint32_t c[2], sc[2];
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
-        c[q] = lane + 64 * q < n ? kPartRow + kPartSlot * (uint32_t)(__popcll(m0[q]) + __popcll(m1[q]))
-                                 : 0u;
+    for (int q = 0; q < 2; ++q) {
+        const uint32_t sl = (uint32_t)(__popcll(m0[q]) + __popcll(m1[q]));
+        c[q] = lane + 64 * q < n ? (sl == 1 ? c_one : c_row + c_slot * sl) : 0u;
+    }
     sc[0] = wave_scan_incl(c[0]);
     const uint32_t tot0 = rl(sc[0], 63);
     sc[1] = wave_scan_incl(c[1]) + tot0;
@@ -1563,7 +1576,7 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
     if (batch >= kPartRangeMin) {
         pr = part_range(ps, batch * TK, IN);
     } else {
-        const PartAssign pa = part_assign(&ps, batch * TK, IN, d.n_experts);
+        const PartAssign pa = part_assign(&ps, batch * TK, IN, d.n_experts, kGuOne, kGuRow, kGuSlot);
         if (pa.u != 0xFFFFFFFFu) pr = PartRange{pa.u * IN + pa.r0, pa.nr};
     }
     const uint32_t N = pr.n;
