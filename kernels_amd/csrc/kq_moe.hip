@@ -1485,18 +1485,18 @@ struct PartRange {
     uint32_t g0, n;
 };
 constexpr uint32_t kPartRangeMin = 8;  // tokens from which the gate/up takes equal-cost ranges
-__device__ __forceinline__ uint32_t range_pos(uint64_t X, const uint32_t (&c)[2],
+__device__ __forceinline__ uint32_t range_pos(uint32_t X, const uint32_t (&c)[2],
                                               const uint32_t (&cu)[2], uint32_t nrows, uint32_t n) {
     const uint32_t lane = threadIdx.x & 63;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const uint32_t u = lane + 64 * q;
-        const uint64_t lo = cu[q], hi = (uint64_t)cu[q] + (uint64_t)nrows * c[q];
+        const uint32_t lo = cu[q], hi = cu[q] + nrows * c[q];
         const uint64_t hit = __ballot(u < n && c[q] > 0 && lo <= X && X < hi);
         if (hit) {  // uniform
             const uint32_t l = (uint32_t)__builtin_ctzll(hit);
             const uint32_t cl = rl(c[q], l), base = rl(cu[q], l);
-            const uint32_t r = (uint32_t)((X - base + cl - 1) / cl);  // first row starting at or after X
+            const uint32_t r = (X - base + cl - 1) / cl;  // first row starting at or after X
             return (l + 64 * q) * nrows + r;                         // r == nrows: the next entry's row 0
         }
     }
@@ -1519,9 +1519,11 @@ __device__ __forceinline__ PartRange part_range(const Plan& ps, uint32_t nslots,
     const uint32_t i1 = wave_scan_incl(nrows * c[1]) + tot0;
     cu[0] = i0 - nrows * c[0];
     cu[1] = i1 - nrows * c[1];
-    const uint64_t W = rl(i1, 63);
-    const uint32_t s = range_pos(W * b / G, c, cu, nrows, n);
-    const uint32_t e = range_pos(W * (b + 1) / G, c, cu, nrows, n);
+    // the boundaries floor(W b / G) in 32 bits: (W / G) b + (W % G) b / G
+    // (32-bit arithmetic: the 64-bit divisions cost ~0.4 us of the prologue)
+    const uint32_t W = rl(i1, 63), Wq = W / G, Wr = W - Wq * G;
+    const uint32_t s = range_pos(Wq * b + Wr * b / G, c, cu, nrows, n);
+    const uint32_t e = range_pos(Wq * (b + 1) + Wr * (b + 1) / G, c, cu, nrows, n);
     return PartRange{s, e - s};
 }
 
@@ -1556,13 +1558,27 @@ __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t half = lane >> 5, rowb = K >> 1, metab = (K >> 6) * 2;
 
-    // 1. every token's x (K <= 4096, batch <= 16: at most kStXr words per thread)
+    // 1. the logits of the wave's tokens (t = wave, wave + 8), then every
+    // token's x (K <= 4096, batch <= 16: at most kStXr words per thread). The
+    // logits go first, so the top-k waits for them alone (loads retire in
+    // order) and not for the x of every token; every wave loads both sets
+    // (clamped to a valid token), so the wait counts are exact.
+    const uint32_t NE = d.n_experts;
+    float lgv[2][4];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const uint32_t t = min(wave + r * kStWaves, batch - 1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) lgv[r][q] = lg[(size_t)t * NE + min(lane + 64 * q, NE - 1)];
+    }
     StStage st;
     st_stage_load(st, xh, batch, K);
     // 2. top-k of every token, then the plan
-    for (uint32_t t = wave; t < batch; t += kStWaves)
-        topk_wave<false>(lg + (size_t)t * d.n_experts, d.n_experts, TK, s_idx + t * TK,
-                         s_wgt + t * TK);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const uint32_t t = wave + r * kStWaves;
+        if (t < batch) topk_vals(lgv[r], NE, TK, s_idx + t * TK, s_wgt + t * TK);  // uniform
+    }
     __syncthreads();
     build_plan(s_idx, batch * TK, d.n_experts, ps, bits);
     if (blockIdx.x == 0) publish_plan(ps, s_idx, s_wgt, batch * TK, idx_out, wgt_out, plan_out);
