@@ -1520,7 +1520,7 @@ __device__ __forceinline__ PartRange part_range(const Plan& ps, uint32_t nslots,
     cu[0] = i0 - nrows * c[0];
     cu[1] = i1 - nrows * c[1];
     // the boundaries floor(W b / G) in 32 bits: (W / G) b + (W % G) b / G
-    // (32-bit arithmetic: the 64-bit divisions cost ~0.4 us of the prologue)
+    // (32-bit arithmetic: the 64-bit divisions cost ~0.26 us of the prologue)
     const uint32_t W = rl(i1, 63), Wq = W / G, Wr = W - Wq * G;
     const uint32_t s = range_pos(Wq * b + Wr * b / G, c, cu, nrows, n);
     const uint32_t e = range_pos(Wq * (b + 1) + Wr * (b + 1) / G, c, cu, nrows, n);
@@ -1540,8 +1540,8 @@ __device__ __forceinline__ PartRange part_range(const Plan& ps, uint32_t nslots,
 // logits-only router launch before this one): every workgroup runs the
 // top-k of every token (wave w takes tokens w, w + 8) and builds the plan in
 // LDS; workgroup 0 publishes idx, wgt and the plan for the down launch.
-// Every token's x is loaded at entry, ahead of the logits, and staged in LDS
-// by token, so the staging never waits behind the weight ring.
+// Every token's x is loaded at entry, right after the wave's logits, and
+// staged in LDS by token, so the staging never waits behind the weight ring.
 template <int J>
 __global__ __launch_bounds__(64 * kStWaves) void moe_gu_part_k(
     const uint8_t* __restrict__ pool, kq_moe_desc d, const uint16_t* __restrict__ xh,
