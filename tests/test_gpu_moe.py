@@ -494,6 +494,65 @@ def test_other_shapes(gpu, hidden, inter, batch):
     assert_close(to_f64(b.y), Yd, atol=1e-4, rtol=1e-4, what=f"down {hidden}x{inter} b{batch}")
 
 
+# (experts, top-k, tokens): the most slots a call can have, 16 tokens x top-8
+# of 256 experts (128 slots, over 100 distinct experts: plan entries past 64,
+# slots in both words of the masks), and one slot a token (top-1), at every
+# token count form of the block (streaming 1, whole-entry split 5, equal-cost
+# ranges 8 and 16)
+SLOT_EXTREMES = [(256, 8, 1), (256, 8, 5), (256, 8, 8), (256, 8, 16),
+                 (64, 1, 1), (64, 1, 5), (64, 1, 8), (64, 1, 16)]
+
+
+@pytest.fixture(scope="module")
+def slot_pools(gpu):
+    """Pools of 256 x top-8 and 64 x top-1 experts, hidden = inter = 256."""
+    out = {}
+    for ne, tk in sorted({(e, k) for e, k, _ in SLOT_EXTREMES}):
+        d, off = _compact_desc(256, 256, ne, tk)
+        host = gen.moe_pool(ne, seed=ne + tk, quantize=True, hidden=256, inter=256, blob=d.blob,
+                            off=off)
+        out[(ne, tk)] = (d, host, dev(host, gpu))
+    return out
+
+
+@pytest.mark.parametrize("ne,tk,batch", SLOT_EXTREMES)
+def test_block_slot_extremes(gpu, slot_pools, ne, tk, batch):
+    """The block, and the standalone projections from its routing, against
+    the oracle at the slot extremes (routing exact); at one token also the
+    one-launch, atomic sum(h) and unfused forms."""
+    d, host, pool = slot_pools[(ne, tk)]
+    R, X = gen.moe_inputs(ne, hidden=256, batch=batch, seed=1000 * tk + 10 * batch)
+    oidx, owgt, lg = oracle.moe_router(R, oracle.F16, X, oracle.F16, batch, odesc(d))
+    assert routing_margin(lg, tk) > 1e-5
+    _, _, Yref = oracle.moe_block(host, odesc(d), R, oracle.F16, X, oracle.F16, batch)
+    Rd, Xd = dev(R, gpu).view(torch.float16), dev(X, gpu).view(torch.float16)
+    paths = [None] + ([kq.MOE_PATH_ONE, kq.MOE_PATH_ATOMIC] if batch == 1 else [])
+    for path in paths:
+        b = Block(gpu, d, batch)
+        kq.moe_block(pool, d, Rd, Xd, b.idx, b.wgt, b.H, b.y, b.ws, b.wsb, batch=batch, path=path)
+        torch.cuda.synchronize()
+        what = f"{ne} experts top-{tk} b{batch} path {path}"
+        assert np.array_equal(b.idx.cpu().numpy().astype(np.uint32), oidx), what
+        assert np.allclose(b.wgt.cpu().numpy(), owgt, atol=1e-6), what
+        assert_close(to_f64(b.y), Yref, what=what)
+    kq.moe_gate_up_swiglu(pool, d, b.idx, Xd, b.H, b.ws, b.wsb, batch=batch)
+    torch.cuda.synchronize()
+    Href = oracle.moe_gate_up(host, odesc(d), oidx, X, oracle.F16, batch)
+    assert_close(to_f64(b.H), Href, what=f"h {ne} experts top-{tk} b{batch}")
+    kq.moe_down_combine(pool, d, b.idx, b.wgt, b.H, b.y, b.ws, b.wsb, batch=batch)
+    torch.cuda.synchronize()
+    Yd = oracle.moe_down(host, odesc(d), oidx, b.wgt.cpu().numpy().astype(np.float64),
+                         host_bits(b.H, np.uint16), batch)
+    assert_close(to_f64(b.y), Yd, atol=1e-4, rtol=1e-4, what=f"down {ne} experts top-{tk} b{batch}")
+    if batch == 1:
+        b = Block(gpu, d, 1)
+        ws, wsb = unfused_ws(gpu, d)
+        kq.moe_block_unfused(pool, d, Rd, Xd, b.idx, b.wgt, b.H, b.y, ws, wsb)
+        torch.cuda.synchronize()
+        assert np.array_equal(b.idx.cpu().numpy().astype(np.uint32), oidx)
+        assert_close(to_f64(b.y), Yref, what=f"unfused {ne} experts top-{tk}")
+
+
 def test_unfused_fp32_inputs_and_fp16_out(gpu, pool16):
     """The one-op-per-launch block with fp32 router and x (xh written by its
     router launch) and an fp16 output, against the oracle and the fused
