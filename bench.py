@@ -28,6 +28,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sections ...]
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -780,52 +781,59 @@ def bench_skinny(torch, kq, dev, args, timer, ceil, res):
     --skinny-batches tokens through the vector path, the matrix cores and
     AUTO's choice, each a HIP graph over enough weight copies (8 for the
     config-2 shapes, at most 256) that ~940 MB of weights stream per replay,
-    so every byte comes from HBM; every (tokens, path) of a shape is timed
-    round-robin with the streaming read of the weights' bytes over as many
-    buffers."""
+    so every byte comes from HBM. The token counts of one path form one
+    rotation, round-robin with the streaming read of the weights' bytes over
+    as many buffers, as the reference rotates the variants of one kernel
+    (int4-gemv/src/main.mm:496-521): in one rotation of every path, the
+    vector path's long passes at 8-16 tokens (0.1-0.2 ms a launch) left the
+    matrix-core spans after them 4-10% slower than in a rotation of their
+    own, measured on one box."""
     out = {}
     batches = [int(b) for b in args.skinny_batches.split(",")]
     shapes = [tuple(int(v) for v in sh.split("x")) for sh in args.skinny_shapes.split(",")]
+    paths = (("valu", kq.PATH_VALU), ("mfma", kq.PATH_MFMA), ("auto", kq.PATH_AUTO))
     for M, K in shapes:
         ncopy = max(8, min(256, int(940e6 // (M * K // 2))))
         layers = make_int4_layers(torch, dev, ncopy, [("w", M, K)], seed=M)
-        variants, holds, keys = {}, [], []
-        for batch in batches:
-            x = torch.randn((batch, K), device=dev).half()
-            y = torch.empty((batch, M), dtype=torch.float16, device=dev)
-            for pname, path in (("valu", kq.PATH_VALU), ("mfma", kq.PATH_MFMA), ("auto", kq.PATH_AUTO)):
-                def one(path=path, x=x, y=y, batch=batch):
+        wb = int4_bytes(M, K, 0)
+        cv, chold = ceil.variant(f"skinny_{M}x{K}", wb, ncopy)
+        xs = {batch: torch.randn((batch, K), device=dev).half() for batch in batches}
+        ys = {batch: torch.empty((batch, M), dtype=torch.float16, device=dev) for batch in batches}
+        rows = {batch: {} for batch in batches}
+        ceil_us = []
+        for pname, path in paths:
+            variants, holds = {}, []
+            for batch in batches:
+                def one(path=path, x=xs[batch], y=ys[batch], batch=batch):
                     for L in layers:
                         W, SB, _, _ = L["w"]
                         kq.int4_gemv(W, SB, x, y, kq.GemvParams(M, K, G), batch=batch, path=path)
                 try:
                     one()
                 except kq.KQError:
-                    keys.append((batch, pname, None))
                     continue
                 g = graph_of(torch, one)
-                holds += [g, x, y]
-                variants[(batch, pname)] = (g.replay, 2, ncopy)
-                keys.append((batch, pname, True))
-        wb = int4_bytes(M, K, 0)
-        cv, hold = ceil.variant(f"skinny_{M}x{K}", wb, ncopy)
-        holds.append(hold)
-        variants["ceiling"] = cv
-        r = timer.round_robin(variants, rounds=5)
-        for batch in batches:
-            row = {}
-            for pname in ("valu", "mfma", "auto"):
-                if (batch, pname) not in r:
-                    row[pname] = None
+                holds.append(g)
+                variants[batch] = (g.replay, 2, ncopy)
+            variants["ceiling"] = cv
+            r = timer.round_robin(variants, rounds=5)
+            ceil_us.append(r["ceiling"])
+            for batch in batches:
+                if batch not in r:
+                    rows[batch][pname] = None
                     continue
-                k = r[(batch, pname)]
+                k = r[batch]
                 b = int4_bytes(M, K, batch)
-                row[pname] = dict(us=k["us"], us_best=k["us_best"], gbs=round(b / k["us"] / 1e3, 1),
-                                  of_ceiling=round(r["ceiling"]["us"] / k["us"], 4))
-            out[f"{M}x{K}_b{batch}"] = row
-        out[f"{M}x{K}_ceiling"] = dict(us=r["ceiling"]["us"], us_best=r["ceiling"]["us_best"],
+                rows[batch][pname] = dict(us=k["us"], us_best=k["us_best"],
+                                          gbs=round(b / k["us"] / 1e3, 1),
+                                          of_ceiling=round(r["ceiling"]["us"] / k["us"], 4))
+            del variants, holds
+        for batch in batches:
+            out[f"{M}x{K}_b{batch}"] = rows[batch]
+        out[f"{M}x{K}_ceiling"] = dict(us=statistics.median(c["us"] for c in ceil_us),
+                                       us_best=min(c["us_best"] for c in ceil_us),
                                        bytes=wb, copies=ncopy)
-        del layers, holds, variants
+        del layers, chold, xs, ys
         torch.cuda.empty_cache()
     res["skinny"] = out
 
