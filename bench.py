@@ -226,11 +226,15 @@ def bench_int4_step(torch, kq, dev, args, timer, ceil, res):
         per[sh] = dict(us=k["us"], us_best=k["us_best"], gbs=round(b / k["us"] / 1e3, 1),
                        frac=round(b / k["us"] / 1e3 / HBM_PEAK_GBS, 4), bytes=b,
                        **vs_ceiling(k, r[f"int4_{b / 1e6:.2f}MB"], r[f"out_{sh}"]))
-    # the step's own ceiling: its 224 reads at the per-shape ceilings
+    # the step's own ceilings: its 224 reads at the per-shape ceilings, and
+    # the same with each GEMV's y stored
     step_ceil_us = N_LAYERS * sum(r[f"int4_{int4_bytes(M, K) / 1e6:.2f}MB"]["us"]
                                   for _, M, K in LLAMA)
+    step_ceil_out_us = N_LAYERS * sum(r[f"out_{M}x{K}"]["us"] for _, M, K in LLAMA)
     res["step"]["ceiling_ms"] = round(step_ceil_us / 1e3, 4)
     res["step"]["of_ceiling"] = round(step_ceil_us / 1e3 / ms, 4)
+    res["step"]["ceiling_out_ms"] = round(step_ceil_out_us / 1e3, 4)
+    res["step"]["of_ceiling_out"] = round(step_ceil_out_us / 1e3 / ms, 4)
     res["per_shape"] = per
     del holds, variants
 
@@ -1017,6 +1021,8 @@ def main():
                                                                             HBM_PEAK_GBS, 4)},
         "roofline": res.get("roofline"),
         "cpu_baseline": cpu,
+        "step": {k: st[k] for k in ("ceiling_ms", "of_ceiling", "ceiling_out_ms", "of_ceiling_out",
+                                    "round_robin_ms", "round_robin_ms_best") if k in st} or None,
         "per_shape": res.get("per_shape"),
         "step_fused_projections": res.get("step_fused"),
         "launch_floor": res.get("launch_floor"),
