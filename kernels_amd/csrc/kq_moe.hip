@@ -611,9 +611,7 @@ __global__ __launch_bounds__(kGuThreads) void moe_gate_up_k(
 #pragma unroll
         for (int r = 0; r < kGuRW; ++r) {
             if (lane == (uint32_t)r && m0 + r < IN) {
-                const float gg = fminf(g[r] + bf2f((uint16_t)bg_raw), 7.0f);
-                const float uu = fminf(fmaxf(up[r] + bf2f((uint16_t)bu_raw), -7.0f), 7.0f);
-                const float h = (gg / (1.0f + expf(-1.702f * gg))) * (uu + 1.0f);
+                const float h = swiglu(g[r] + bf2f((uint16_t)bg_raw), up[r] + bf2f((uint16_t)bu_raw));
                 H[(size_t)slot * IN + m0 + r] = f2h(h);
             }
         }
