@@ -294,8 +294,8 @@ kq_status kq_moe_block(const uint8_t* pool, const kq_moe_desc* d,
  * does, the three passes of encodeFused (moe-fused/src/main.mm:176-206).
  * KQ_MOE_PATH_ONE: one token, the whole block in one launch of one
  * workgroup per CU (router logits exchanged through tagged device-coherent
- * stores, h through one grid-wide barrier); inside a graph 0.3-0.5 us a
- * block faster than three launches (about 20.9 against 21.3 us at the
+ * stores, h through one grid-wide barrier); inside a graph 0.3-0.6 us a
+ * block faster than three launches (about 20.7 against 21.3 us at the
  * gpt-oss-120b shape), two launches fewer for eager callers. It stays an
  * option rather than the default for its residency demand. Every workgroup must
  * be resident at once: the path is refused (KQ_EUNSUPPORTED) when the
